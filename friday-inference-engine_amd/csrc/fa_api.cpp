@@ -1,0 +1,279 @@
+// C-ABI layer of libfriday_attn: argument validation (before any HIP call),
+// status codes instead of the reference's exceptions/abort, and the host-side
+// RoPE table. Entry points are declared and documented in include/friday_attn.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/friday_attn.h"
+#include "fa_internal.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return FA_OK;
+}
+
+int launch_status(int rc, const char* what) {
+    if (rc == -2) return fail(FA_ERR_UNSUPPORTED, "%s: unsupported configuration", what);
+    if (rc != 0) {
+        const hipError_t e = hipGetLastError();
+        return fail(FA_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    }
+    return ok();
+}
+
+bool head_dim_ok(int d) { return d == 64 || d == 128; }
+
+// Shape rules of the reference launchers (attention_kernels.cu:416-419, 450-454).
+int check_heads(const char* what, int Hq, int Hkv, int d) {
+    if (!head_dim_ok(d)) return fail(FA_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128 (got %d)", what, d);
+    if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0)
+        return fail(FA_ERR_INVALID, "%s: invalid shape (num_heads %d, num_kv_heads %d)", what, Hq, Hkv);
+    return FA_OK;
+}
+
+// One RoPE angle pair, written with the formula of friday_cpu::rope (cpu_ops.cpp:29-32).
+void rope_fill(float* table, int max_ctx, int head_dim, float freq_base, const float* ff) {
+    const int hd2 = head_dim / 2;
+    for (int i = 0; i < hd2; ++i) {
+        const float den = std::pow(freq_base, (2.0f * (float)i) / (float)head_dim);
+        for (int p = 0; p < max_ctx; ++p) {
+            float theta = (float)p / den;
+            if (ff) theta /= ff[i];
+            float* e = table + ((size_t)p * hd2 + i) * 2;
+            e[0] = std::cos(theta);
+            e[1] = std::sin(theta);
+        }
+    }
+}
+
+size_t split_ws_bytes(int batch, int Hq, int max_seq, int d) {
+    const size_t ns = (size_t)fa::split_count(max_seq);
+    return (size_t)batch * Hq * ns * ((size_t)d + 2) * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* friday_attn_last_error(void) { return g_err.c_str(); }
+
+int friday_attn_version(void) { return 100; }
+
+// ---------------- RoPE table ----------------
+
+size_t friday_attn_rope_table_bytes(int max_ctx, int head_dim) {
+    if (max_ctx <= 0 || head_dim <= 0 || head_dim % 2) return 0;
+    return (size_t)max_ctx * (head_dim / 2) * 2 * sizeof(float);
+}
+
+int friday_attn_rope_table_fill_host(float* table, int max_ctx, int head_dim, float freq_base,
+                                     const float* freq_factors_host) {
+    if (!table || max_ctx <= 0 || !head_dim_ok(head_dim) || !(freq_base > 0.0f))
+        return fail(FA_ERR_INVALID, "rope_table_fill_host: invalid arguments");
+    rope_fill(table, max_ctx, head_dim, freq_base, freq_factors_host);
+    return ok();
+}
+
+int friday_attn_rope_table_upload(float* d_table, int max_ctx, int head_dim, float freq_base,
+                                  const float* freq_factors_host, void* stream) {
+    if (!d_table || max_ctx <= 0 || !head_dim_ok(head_dim) || !(freq_base > 0.0f))
+        return fail(FA_ERR_INVALID, "rope_table_upload: invalid arguments");
+    std::vector<float> host((size_t)max_ctx * head_dim);
+    rope_fill(host.data(), max_ctx, head_dim, freq_base, freq_factors_host);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (hipMemcpyAsync(d_table, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return fail(FA_ERR_LAUNCH, "rope_table_upload: copy failed: %s", hipGetErrorString(hipGetLastError()));
+    return ok();
+}
+
+// ---------------- append ----------------
+
+int friday_attn_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
+                              const int* d_pos, int pos, int T, int head_dim, int num_q_heads, int num_kv_heads,
+                              int max_ctx, const float* rope_table, int neox, void* stream) {
+    const char* w = "rope_store_kv";
+    if (int rc = check_heads(w, num_q_heads, num_kv_heads, head_dim)) return rc;
+    if (T <= 0 || max_ctx <= 0 || !q || !k || !rope_table) return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if ((k_layer == nullptr) != (v_layer == nullptr) || (k_layer && !v))
+        return fail(FA_ERR_INVALID, "%s: k_layer, v_layer and v must be given together", w);
+    if (!d_pos && (pos < 0 || pos + T > max_ctx))
+        return fail(FA_ERR_INVALID, "%s: positions [%d, %d) exceed max_ctx %d", w, pos, pos + T, max_ctx);
+    fa::RopeParams p{};
+    p.q = q; p.k = k; p.v = v; p.k_dst = k_layer; p.v_dst = v_layer; p.table = rope_table;
+    p.d_pos = d_pos; p.pos = pos; p.T = T; p.D = head_dim; p.Hq = num_q_heads; p.Hkv = num_kv_heads;
+    p.max_ctx = max_ctx; p.neox = neox ? 1 : 0;
+    return launch_status(fa::launch_rope_store(p, false, static_cast<hipStream_t>(stream)), w);
+}
+
+int friday_attn_store_kv_q8(const uint16_t* k, const uint16_t* v, int8_t* k_layer, uint16_t* k_scale,
+                            int8_t* v_layer, uint16_t* v_scale, const int* d_pos, int pos, int T, int kv_dim,
+                            int max_ctx, void* stream) {
+    const char* w = "store_kv_q8";
+    if (!k || !v || !k_layer || !k_scale || !v_layer || !v_scale || T <= 0 || max_ctx <= 0)
+        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if (kv_dim <= 0 || kv_dim % 32) return fail(FA_ERR_INVALID, "%s: kv_dim must be a multiple of 32", w);
+    if (!d_pos && (pos < 0 || pos + T > max_ctx))
+        return fail(FA_ERR_INVALID, "%s: positions [%d, %d) exceed max_ctx %d", w, pos, pos + T, max_ctx);
+    fa::Q8StoreParams p{};
+    p.k = k; p.v = v; p.k_dst = k_layer; p.ks_dst = k_scale; p.v_dst = v_layer; p.vs_dst = v_scale;
+    p.d_pos = d_pos; p.pos = pos; p.T = T; p.kv_dim = kv_dim; p.max_ctx = max_ctx;
+    return launch_status(fa::launch_store_kv_q8(p, static_cast<hipStream_t>(stream)), w);
+}
+
+// ---------------- decode ----------------
+
+static int decode_common(const char* w, const uint16_t* q, const void* k, const void* v, uint16_t* out, int seq_len,
+                         const int* d_pos, int max_seq, int Hq, int Hkv, int d, void* ws, size_t ws_bytes,
+                         bool single, const uint16_t* ks, const uint16_t* vs, void* stream) {
+    if (int rc = check_heads(w, Hq, Hkv, d)) return rc;
+    if (!q || !k || !v || !out) return fail(FA_ERR_INVALID, "%s: null tensor", w);
+    if (max_seq <= 0) return fail(FA_ERR_INVALID, "%s: invalid max_seq_len %d", w, max_seq);
+    if (!d_pos && (seq_len <= 0 || seq_len > max_seq))
+        return fail(FA_ERR_INVALID, "%s: seq_len %d outside [1, %d]", w, seq_len, max_seq);
+    const bool q8 = ks && vs;
+    if ((ks == nullptr) != (vs == nullptr)) return fail(FA_ERR_INVALID, "%s: give both k_scale and v_scale", w);
+    const int G = Hq / Hkv;
+    fa::DecodeParams p{};
+    p.q = q; p.k = k; p.v = v; p.k_scale = ks; p.v_scale = vs; p.d_pos = d_pos;
+    p.seq_len = d_pos ? 0 : seq_len;
+    p.max_seq = max_seq;
+    p.out = out; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.ngb = (G + 15) / 16; p.kv_dim = Hkv * d;
+    p.single = single ? 1 : 0;
+    p.scale2 = (1.0f / std::sqrt((float)d)) * 1.4426950408889634f;
+    if (!single) {
+        // host length: the grid only needs the splits of seq_len
+        const int grid_len = d_pos ? max_seq : seq_len;
+        p.nsplit_grid = fa::split_count(grid_len);
+        const size_t need = split_ws_bytes(1, Hq, grid_len, d);
+        if (!ws || ws_bytes < need)
+            return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, ws_bytes);
+        p.part_o = static_cast<float*>(ws);
+        p.part_ml = p.part_o + (size_t)Hq * p.nsplit_grid * d;
+    } else {
+        p.nsplit_grid = 1;
+    }
+    return launch_status(fa::launch_decode(p, d, 1, false, q8, static_cast<hipStream_t>(stream)), w);
+}
+
+int friday_attn_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                                 int seq_len, int num_heads, int num_kv_heads, int head_dim, void* stream) {
+    return decode_common("decode_attention", q, k_cache, v_cache, out, seq_len, nullptr, seq_len > 0 ? seq_len : 1,
+                         num_heads, num_kv_heads, head_dim, nullptr, 0, true, nullptr, nullptr, stream);
+}
+
+int friday_attn_decode_attention_dev_pos(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                         uint16_t* out, const int* d_pos, int max_seq_len, int num_heads,
+                                         int num_kv_heads, int head_dim, void* stream) {
+    if (!d_pos) return fail(FA_ERR_INVALID, "decode_attention_dev_pos: d_pos is null");
+    return decode_common("decode_attention_dev_pos", q, k_cache, v_cache, out, 0, d_pos, max_seq_len, num_heads,
+                         num_kv_heads, head_dim, nullptr, 0, true, nullptr, nullptr, stream);
+}
+
+int friday_attn_decode_fits_shared_memory(int max_seq_len) { return max_seq_len > 0 ? 1 : 0; }
+
+size_t friday_attn_split_workspace_bytes(int num_heads, int max_seq_len) {
+    if (num_heads <= 0 || max_seq_len <= 0) return 0;
+    return split_ws_bytes(1, num_heads, max_seq_len, 128);
+}
+
+int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out,
+                                       int seq_len, const int* d_pos, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                       void* stream, const uint16_t* k_scale, const uint16_t* v_scale) {
+    return decode_common("decode_attention_split", q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads,
+                         num_kv_heads, head_dim, workspace, workspace_bytes, false, k_scale, v_scale, stream);
+}
+
+// ---------------- prefill ----------------
+
+int friday_attn_prefill_supported(int num_heads, int num_kv_heads, int head_dim) {
+    return head_dim_ok(head_dim) && num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0 ? 1 : 0;
+}
+
+int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out, int T,
+                                  const int* d_pos0, int num_heads, int num_kv_heads, int head_dim, void* stream,
+                                  const uint16_t* k_scale, const uint16_t* v_scale) {
+    const char* w = "prefill_attention";
+    if (T <= 0) return ok();  // the reference launcher returns early (attention_kernels.cu:656)
+    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
+    if (!q || !k_cache || !v_cache || !out || !d_pos0) return fail(FA_ERR_INVALID, "%s: null argument", w);
+    if ((k_scale == nullptr) != (v_scale == nullptr)) return fail(FA_ERR_INVALID, "%s: give both scales", w);
+    fa::PrefillParams p{};
+    p.q = q; p.k = k_cache; p.v = v_cache; p.k_scale = k_scale; p.v_scale = v_scale; p.out = out;
+    p.d_pos0 = d_pos0; p.T = T; p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = num_heads / num_kv_heads;
+    p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
+    return launch_status(fa::launch_prefill(p, head_dim, k_scale != nullptr, static_cast<hipStream_t>(stream)), w);
+}
+
+// ---------------- paged ----------------
+
+size_t friday_attn_paged_workspace_bytes(int batch, int num_heads, int max_seq_len) {
+    if (batch <= 0 || num_heads <= 0 || max_seq_len <= 0) return 0;
+    return split_ws_bytes(batch, num_heads, max_seq_len, 128);
+}
+
+int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_pool, uint16_t* v_pool,
+                                    const int32_t* block_table, int block_table_stride, const int32_t* seq_lens,
+                                    int batch, int head_dim, int num_q_heads, int num_kv_heads, int max_ctx,
+                                    const float* rope_table, int neox, void* stream) {
+    const char* w = "paged_rope_store_kv";
+    if (int rc = check_heads(w, num_q_heads, num_kv_heads, head_dim)) return rc;
+    if (batch <= 0 || max_ctx <= 0 || !q || !k || !v || !k_pool || !v_pool || !block_table || !seq_lens ||
+        !rope_table || block_table_stride * FA_PAGE_TOKENS < max_ctx)
+        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    fa::RopeParams p{};
+    p.q = q; p.k = k; p.v = v; p.k_dst = k_pool; p.v_dst = v_pool; p.table = rope_table;
+    p.block_table = block_table; p.bt_stride = block_table_stride; p.seq_lens = seq_lens;
+    p.T = batch; p.D = head_dim; p.Hq = num_q_heads; p.Hkv = num_kv_heads; p.max_ctx = max_ctx;
+    p.neox = neox ? 1 : 0;
+    return launch_status(fa::launch_rope_store(p, true, static_cast<hipStream_t>(stream)), w);
+}
+
+int friday_attn_paged_decode_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                                       uint16_t* out, const int32_t* block_table, int block_table_stride,
+                                       const int32_t* seq_lens, int batch, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+    const char* w = "paged_decode_attention";
+    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
+    if (batch <= 0 || max_seq_len <= 0 || !q || !k_pool || !v_pool || !out || !block_table || !seq_lens)
+        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if ((long long)block_table_stride * FA_PAGE_TOKENS < max_seq_len)
+        return fail(FA_ERR_INVALID, "%s: block_table_stride %d cannot address max_seq_len %d", w,
+                    block_table_stride, max_seq_len);
+    const int G = num_heads / num_kv_heads;
+    fa::DecodeParams p{};
+    p.q = q; p.k = k_pool; p.v = v_pool; p.block_table = block_table; p.bt_stride = block_table_stride;
+    p.seq_lens = seq_lens; p.max_seq = max_seq_len; p.out = out;
+    p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = G; p.ngb = (G + 15) / 16; p.kv_dim = num_kv_heads * head_dim;
+    p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
+    p.nsplit_grid = fa::split_count(max_seq_len);
+    const size_t need = split_ws_bytes(batch, num_heads, max_seq_len, head_dim);
+    if (!workspace || workspace_bytes < need)
+        return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
+    p.part_o = static_cast<float*>(workspace);
+    p.part_ml = p.part_o + (size_t)batch * num_heads * p.nsplit_grid * head_dim;
+    return launch_status(fa::launch_decode(p, head_dim, batch, true, false, static_cast<hipStream_t>(stream)), w);
+}
+
+}  // extern "C"

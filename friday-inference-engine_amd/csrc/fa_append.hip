@@ -1,0 +1,115 @@
+// KV append for gfx950: RoPE on q and k at the token's position, rotated k and
+// raw v stored into the layer cache (contiguous or paged), and the int8 cache
+// variant.
+//
+// Rotation (cpu_ops.cpp:26-43, cuda_math_kernels.cu:363-404):
+//   x0' = x0*c - x1*s, x1' = x0*s + x1*c in fp32, NaN -> 0, clamp +-65504, RNE fp16;
+//   neox pairs (i, i + d/2), otherwise (2i, 2i + 1).
+// (c, s) come from the host-built table (fa_rope_table.cpp) and the products are
+// not contracted into FMAs, so the stored bits equal the reference CPU path's.
+#include "fa_common.hpp"
+#include "fa_internal.hpp"
+
+namespace fa {
+namespace {
+
+__device__ __forceinline__ float rot_clamp(float r) {
+    if (__builtin_isnan(r)) return 0.0f;
+    return fminf(fmaxf(r, -65504.0f), 65504.0f);
+}
+
+// One thread per (token, head, rotation pair). Heads [0, Hq) are query heads,
+// [Hq, Hq + Hkv) key heads (their thread also moves the matching v pair).
+template <bool PAGED>
+__global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.y;
+    const int hd2 = p.D >> 1;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (p.Hq + p.Hkv) * hd2) return;
+    const int h = idx / hd2, i = idx - h * hd2;
+    const int pos = PAGED ? p.seq_lens[t] - 1 : (p.d_pos ? *p.d_pos : p.pos) + t;
+    if (pos < 0 || pos >= p.max_ctx) return;
+    const float2 cs = reinterpret_cast<const float2*>(p.table)[(size_t)pos * hd2 + i];
+    const int o0 = p.neox ? i : 2 * i;
+    const int o1 = p.neox ? i + hd2 : 2 * i + 1;
+    const int kv_dim = p.Hkv * p.D;
+    const bool is_k = h >= p.Hq;
+    _Float16* x = is_k ? reinterpret_cast<_Float16*>(p.k) + (size_t)t * kv_dim + (h - p.Hq) * p.D
+                       : reinterpret_cast<_Float16*>(p.q) + (size_t)t * p.Hq * p.D + h * p.D;
+    const float a = (float)x[o0], b = (float)x[o1];
+    const float ac = a * cs.x, bs = b * cs.y, as = a * cs.y, bc = b * cs.x;
+    const _Float16 r0 = (_Float16)rot_clamp(ac - bs);
+    const _Float16 r1 = (_Float16)rot_clamp(as + bc);
+    x[o0] = r0;
+    x[o1] = r1;
+    if (is_k && p.k_dst) {
+        size_t row;
+        if (PAGED) {
+            const int phys = p.block_table[(size_t)t * p.bt_stride + (pos >> 4)];
+            row = (size_t)phys * kPageTokens + (pos & 15);
+        } else {
+            row = (size_t)pos;
+        }
+        const size_t off = row * kv_dim + (size_t)(h - p.Hq) * p.D;
+        _Float16* kd = reinterpret_cast<_Float16*>(p.k_dst) + off;
+        _Float16* vd = reinterpret_cast<_Float16*>(p.v_dst) + off;
+        const _Float16* vs = reinterpret_cast<const _Float16*>(p.v) + (size_t)t * kv_dim + (h - p.Hq) * p.D;
+        kd[o0] = r0;
+        kd[o1] = r1;
+        vd[o0] = vs[o0];
+        vd[o1] = vs[o1];
+    }
+}
+
+// int8 append (cuda_math_kernels.cu:409-432): 32 lanes per 32-value block,
+// K blocks first, then V. dh = fp16(amax / 127); q = clamp(rne(x * (1/dh)), +-127).
+__global__ __launch_bounds__(256) void fa_store_kv_q8_kernel(Q8StoreParams p) {
+    const int lane = threadIdx.x & 31;
+    const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int nblk = p.kv_dim / 32;
+    const int t = blockIdx.y;
+    const int pos = (p.d_pos ? *p.d_pos : p.pos) + t;
+    const bool active = blk < 2 * nblk && pos >= 0 && pos < p.max_ctx;
+    const bool is_v = blk >= nblk;
+    const int bb = is_v ? blk - nblk : blk;
+    float x = 0.0f;
+    if (active) {
+        const uint16_t* src = (is_v ? p.v : p.k) + (size_t)t * p.kv_dim;
+        x = (float)reinterpret_cast<const _Float16*>(src)[bb * 32 + lane];
+        if (__builtin_isnan(x)) x = 0.0f;
+    }
+    float amax = fabsf(x);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    if (!active) return;
+    const _Float16 dh = (_Float16)(amax / 127.0f);
+    const float d = (float)dh;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    int q = (int)rintf(x * inv);
+    q = max(-127, min(127, q));
+    int8_t* dst = (is_v ? p.v_dst : p.k_dst) + (size_t)pos * p.kv_dim;
+    dst[bb * 32 + lane] = (int8_t)q;
+    if (lane == 0) reinterpret_cast<_Float16*>(is_v ? p.vs_dst : p.ks_dst)[(size_t)pos * nblk + bb] = dh;
+}
+
+}  // namespace
+
+int launch_rope_store(const RopeParams& p, bool paged, hipStream_t stream) {
+    const int pairs = (p.Hq + p.Hkv) * (p.D / 2);
+    const dim3 grid((pairs + 255) / 256, p.T);
+    if (paged)
+        hipLaunchKernelGGL(fa_rope_store_kernel<true>, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(fa_rope_store_kernel<false>, grid, dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_store_kv_q8(const Q8StoreParams& p, hipStream_t stream) {
+    const int nblk2 = 2 * (p.kv_dim / 32);
+    const dim3 grid((nblk2 + 7) / 8, p.T);
+    hipLaunchKernelGGL(fa_store_kv_q8_kernel, grid, dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace fa

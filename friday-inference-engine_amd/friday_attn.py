@@ -1,0 +1,294 @@
+"""Python host mirror of the friday_attn C ABI (include/friday_attn.h).
+
+The reference exposes the path as C++ launchers in namespace friday_attn
+(attention_kernels.h:18-50) that throw std::runtime_error on bad input; this
+module binds the C ABI with ctypes and mirrors those launchers under the same
+names (launchDecodeAttention, launchDecodeAttentionSplit, ...), raising
+RuntimeError on a non-zero status. Device memory, copies, streams and events go
+straight to the HIP runtime that libfriday_attn.so links (libamdhip64): this is
+plumbing for tests and the benchmark, not part of the product.
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libfriday_attn.so")
+
+FA_OK = 0
+FA_ERR_INVALID = -1
+FA_ERR_UNSUPPORTED = -2
+FA_ERR_LAUNCH = -3
+FA_ERR_WORKSPACE = -4
+PAGE_TOKENS = 16
+
+# (name, restype, argtypes) of every C-ABI entry point in include/friday_attn.h
+_P, _I, _F, _SZ = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+API = [
+    ("friday_attn_last_error", C.c_char_p, []),
+    ("friday_attn_version", _I, []),
+    ("friday_attn_rope_table_bytes", _SZ, [_I, _I]),
+    ("friday_attn_rope_table_fill_host", _I, [_P, _I, _I, _F, _P]),
+    ("friday_attn_rope_table_upload", _I, [_P, _I, _I, _F, _P, _P]),
+    ("friday_attn_rope_store_kv", _I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _I, _P]),
+    ("friday_attn_store_kv_q8", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("friday_attn_decode_attention", _I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("friday_attn_decode_attention_dev_pos", _I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    ("friday_attn_decode_fits_shared_memory", _I, [_I]),
+    ("friday_attn_split_workspace_bytes", _SZ, [_I, _I]),
+    ("friday_attn_decode_attention_split", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
+    ("friday_attn_prefill_supported", _I, [_I, _I, _I]),
+    ("friday_attn_prefill_attention", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    ("friday_attn_paged_workspace_bytes", _SZ, [_I, _I, _I]),
+    ("friday_attn_paged_rope_store_kv", _I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
+    ("friday_attn_paged_decode_attention", _I,
+     [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+]
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load libfriday_attn.so (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: run __graft_entry__.build() "
+                               f"or python friday-inference-engine_amd/build.py")
+        lib = C.CDLL(path, mode=C.RTLD_GLOBAL)
+        for name, res, args in API:
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+class FridayAttnError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[{status}] {msg}")
+        self.status = status
+
+
+def _check(rc: int):
+    if rc != FA_OK:
+        raise FridayAttnError(rc, load().friday_attn_last_error().decode())
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+# ---------------------------------------------------------------- HIP plumbing
+class Hip:
+    """Minimal ctypes access to the HIP runtime (same libamdhip64 as the library)."""
+
+    _h = None
+
+    @classmethod
+    def lib(cls):
+        if cls._h is None:
+            load()  # pulls in libamdhip64.so.7 with the product library
+            h = C.CDLL("libamdhip64.so.7")
+            h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), _SZ]
+            h.hipFree.argtypes = [_P]
+            h.hipMemcpy.argtypes = [_P, _P, _SZ, _I]
+            h.hipMemcpyAsync.argtypes = [_P, _P, _SZ, _I, _P]
+            h.hipMemset.argtypes = [_P, _I, _SZ]
+            h.hipDeviceSynchronize.argtypes = []
+            h.hipStreamSynchronize.argtypes = [_P]
+            h.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
+            h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+            h.hipEventRecord.argtypes = [_P, _P]
+            h.hipEventSynchronize.argtypes = [_P]
+            h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), _P, _P]
+            h.hipEventDestroy.argtypes = [_P]
+            h.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+            h.hipStreamDestroy.argtypes = [_P]
+            h.hipGetErrorString.restype = C.c_char_p
+            h.hipGetErrorString.argtypes = [_I]
+            h.hipDeviceGetAttribute.argtypes = [C.POINTER(C.c_int), _I, _I]
+            cls._h = h
+        return cls._h
+
+    @classmethod
+    def check(cls, rc, what="hip"):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {cls.lib().hipGetErrorString(rc).decode()}")
+
+    @classmethod
+    def device_count(cls) -> int:
+        n = C.c_int(0)
+        rc = cls.lib().hipGetDeviceCount(C.byref(n))
+        return n.value if rc == 0 else 0
+
+    @classmethod
+    def sync(cls):
+        cls.check(cls.lib().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class DeviceBuffer:
+    """Owned device allocation."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        Hip.check(Hip.lib().hipMalloc(C.byref(p), max(self.nbytes, 1)), f"hipMalloc({self.nbytes})")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        Hip.check(Hip.lib().hipMemcpy(self.ptr + offset, a.ctypes.data, a.nbytes, 1), "hipMemcpy H2D")
+
+    def download(self, shape, dtype, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert offset + out.nbytes <= self.nbytes
+        Hip.check(Hip.lib().hipMemcpy(out.ctypes.data, self.ptr + offset, out.nbytes, 2), "hipMemcpy D2H")
+        return out
+
+    def fill_bytes(self, value: int):
+        Hip.check(Hip.lib().hipMemset(self.ptr, value, self.nbytes), "hipMemset")
+
+    def free(self):
+        if self.ptr:
+            Hip.lib().hipFree(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        e = C.c_void_p()
+        Hip.check(Hip.lib().hipEventCreate(C.byref(e)), "hipEventCreate")
+        self.e = e.value
+
+    def record(self, stream=None):
+        Hip.check(Hip.lib().hipEventRecord(self.e, stream), "hipEventRecord")
+
+    def synchronize(self):
+        Hip.check(Hip.lib().hipEventSynchronize(self.e), "hipEventSynchronize")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        Hip.check(Hip.lib().hipEventElapsedTime(C.byref(ms), self.e, end.e), "hipEventElapsedTime")
+        return ms.value
+
+
+# ------------------------------------------------- friday_attn launcher mirror
+def rope_table_bytes(max_ctx, head_dim) -> int:
+    return load().friday_attn_rope_table_bytes(max_ctx, head_dim)
+
+
+def rope_table_host(max_ctx, head_dim, freq_base, freq_factors=None) -> np.ndarray:
+    t = np.empty((max_ctx, head_dim // 2, 2), np.float32)
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+    _check(load().friday_attn_rope_table_fill_host(t.ctypes.data, max_ctx, head_dim, freq_base,
+                                                   None if ff is None else ff.ctypes.data))
+    return t
+
+
+def rope_table_upload(d_table, max_ctx, head_dim, freq_base, freq_factors=None, stream=None):
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+    _check(load().friday_attn_rope_table_upload(_ptr(d_table), max_ctx, head_dim, freq_base,
+                                                None if ff is None else ff.ctypes.data, stream))
+
+
+def ropeStoreKv(q, k, v, k_layer, v_layer, d_pos, pos, T, head_dim, num_q_heads, num_kv_heads, max_ctx,
+                rope_table, neox, stream=None):
+    """ropeStoreKvKernel launch (cuda_math_kernels.cu:363-404); caches None -> ropeKernel."""
+    _check(load().friday_attn_rope_store_kv(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(v_layer), _ptr(d_pos),
+                                            pos, T, head_dim, num_q_heads, num_kv_heads, max_ctx, _ptr(rope_table),
+                                            int(neox), stream))
+
+
+def storeKvQ8(k, v, k_layer, k_scale, v_layer, v_scale, d_pos, pos, T, kv_dim, max_ctx, stream=None):
+    """storeKvQ8Kernel launch (cuda_math_kernels.cu:409-432)."""
+    _check(load().friday_attn_store_kv_q8(_ptr(k), _ptr(v), _ptr(k_layer), _ptr(k_scale), _ptr(v_layer),
+                                          _ptr(v_scale), _ptr(d_pos), pos, T, kv_dim, max_ctx, stream))
+
+
+def launchDecodeAttention(q, k_cache, v_cache, out, seq_len, num_heads, num_kv_heads, head_dim, stream=None):
+    _check(load().friday_attn_decode_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), seq_len, num_heads,
+                                               num_kv_heads, head_dim, stream))
+
+
+def launchDecodeAttentionDevPos(q, k_cache, v_cache, out, d_pos, max_seq_len, num_heads, num_kv_heads, head_dim,
+                                stream=None):
+    _check(load().friday_attn_decode_attention_dev_pos(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                                       _ptr(d_pos), max_seq_len, num_heads, num_kv_heads,
+                                                       head_dim, stream))
+
+
+def decodeAttentionFitsSharedMemory(max_seq_len) -> bool:
+    return bool(load().friday_attn_decode_fits_shared_memory(max_seq_len))
+
+
+def splitAttentionWorkspaceBytes(num_heads, max_seq_len) -> int:
+    return load().friday_attn_split_workspace_bytes(num_heads, max_seq_len)
+
+
+def launchDecodeAttentionSplit(q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads, num_kv_heads,
+                               head_dim, workspace, stream=None, k_scale=None, v_scale=None, workspace_bytes=None):
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_decode_attention_split(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), seq_len,
+                                                     _ptr(d_pos), max_seq_len, num_heads, num_kv_heads, head_dim,
+                                                     _ptr(workspace), workspace_bytes, stream, _ptr(k_scale),
+                                                     _ptr(v_scale)))
+
+
+def prefillAttentionSupported(num_heads, num_kv_heads, head_dim) -> bool:
+    return bool(load().friday_attn_prefill_supported(num_heads, num_kv_heads, head_dim))
+
+
+def launchPrefillAttention(q, k_cache, v_cache, out, T, d_pos0, num_heads, num_kv_heads, head_dim, stream=None,
+                           k_scale=None, v_scale=None):
+    _check(load().friday_attn_prefill_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), T, _ptr(d_pos0),
+                                                num_heads, num_kv_heads, head_dim, stream, _ptr(k_scale),
+                                                _ptr(v_scale)))
+
+
+def pagedWorkspaceBytes(batch, num_heads, max_seq_len) -> int:
+    return load().friday_attn_paged_workspace_bytes(batch, num_heads, max_seq_len)
+
+
+def pagedRopeStoreKv(q, k, v, k_pool, v_pool, block_table, block_table_stride, seq_lens, batch, head_dim,
+                     num_q_heads, num_kv_heads, max_ctx, rope_table, neox, stream=None):
+    _check(load().friday_attn_paged_rope_store_kv(_ptr(q), _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool),
+                                                  _ptr(block_table), block_table_stride, _ptr(seq_lens), batch,
+                                                  head_dim, num_q_heads, num_kv_heads, max_ctx, _ptr(rope_table),
+                                                  int(neox), stream))
+
+
+def launchPagedDecodeAttention(q, k_pool, v_pool, out, block_table, block_table_stride, seq_lens, batch,
+                               max_seq_len, num_heads, num_kv_heads, head_dim, workspace, stream=None,
+                               workspace_bytes=None):
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_paged_decode_attention(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(out),
+                                                     _ptr(block_table), block_table_stride, _ptr(seq_lens), batch,
+                                                     max_seq_len, num_heads, num_kv_heads, head_dim,
+                                                     _ptr(workspace), workspace_bytes, stream))

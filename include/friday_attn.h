@@ -1,0 +1,140 @@
+/*
+ * friday_attn — MI355X (gfx950) KV-cache path of the FRIDAY inference engine:
+ * RoPE + KV append, GQA decode attention (split-K + log-sum-exp merge), causal
+ * prefill attention on MFMA, and paged multi-sequence decode.
+ *
+ * C ABI. Plain pointers and sizes; fp16 tensors are passed as uint16_t bit
+ * patterns (IEEE binary16), int8 caches as int8_t, `stream` is a hipStream_t
+ * (NULL = the null stream). Every entry point:
+ *   - returns FA_OK (0) or a negative status; friday_attn_last_error() gives the
+ *     message of the calling thread's last failure (the reference throws
+ *     std::runtime_error or aborts at the same points);
+ *   - validates its arguments on the host before any HIP call;
+ *   - never allocates and never synchronises: launches are asynchronous on
+ *     `stream` and may be captured into a HIP graph;
+ *   - reads sequence lengths from device memory when given `d_pos`, so a
+ *     captured launch replays correctly for a new position.
+ *
+ * Layouts (same as the reference Transformer, transformer.cpp:483-503,852-853):
+ *   q, out            [T][num_heads * head_dim]            fp16
+ *   k/v layer cache   [max_ctx][num_kv_heads * head_dim]   fp16, or int8 with
+ *                     fp16 scales [max_ctx][num_kv_heads * head_dim / 32]
+ *   paged pool        [num_pages][16][num_kv_heads * head_dim] fp16, addressed
+ *                     through block_table[seq][pos / 16]
+ * head_dim is 64 or 128 (the reference GPU kernels accept 128 only,
+ * attention_kernels.cu:416); num_heads % num_kv_heads == 0.
+ */
+#ifndef FRIDAY_ATTN_H
+#define FRIDAY_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_OK 0
+#define FA_ERR_INVALID (-1)     /* bad shape / null pointer / out of range */
+#define FA_ERR_UNSUPPORTED (-2) /* valid but not implemented for these shapes */
+#define FA_ERR_LAUNCH (-3)      /* a HIP launch or copy failed */
+#define FA_ERR_WORKSPACE (-4)   /* workspace too small or missing */
+
+#define FA_PAGE_TOKENS 16 /* paged_kv_cache.h:16 KV_BLOCK_SIZE */
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* friday_attn_last_error(void);
+/* Library version, major * 10000 + minor * 100 + patch. */
+int friday_attn_version(void);
+
+/* ---------------- RoPE table (setup) ----------------
+ * The reference evaluates theta_i = pos / base^(2i/d) (/ freq_factors[i]) and
+ * its cos/sin inside ropeStoreKvKernel (cuda_math_kernels.cu:376-381) and
+ * friday_cpu::rope (cpu_ops.cpp:29-32). Here they are evaluated once on the host
+ * with the CPU formula into a table [max_ctx][head_dim/2][2] of float (cos, sin),
+ * which makes the GPU rotation bit-identical to the reference CPU path. */
+size_t friday_attn_rope_table_bytes(int max_ctx, int head_dim);
+int friday_attn_rope_table_fill_host(float* table, int max_ctx, int head_dim, float freq_base,
+                                     const float* freq_factors_host);
+/* Fills on the host and copies into device memory d_table (synchronous; setup only). */
+int friday_attn_rope_table_upload(float* d_table, int max_ctx, int head_dim, float freq_base,
+                                  const float* freq_factors_host, void* stream);
+
+/* ---------------- KV append ----------------
+ * Replaces the launches of ropeStoreKvKernel (cuda_math_kernels.cu:363-404, launched at
+ * transformer.cpp:1046-1048 and :1247-1248) and, with k_layer == v_layer == NULL,
+ * ropeKernel (cuda_math_kernels.cu:331-359). Token t of T sits at position
+ * P + t with P = *d_pos when d_pos != NULL, else P = pos. q [T][Hq*d] and
+ * k [T][Hkv*d] are rotated in place (fp32 math, NaN -> 0, clamp, RNE fp16);
+ * rotated k and raw v are written to row P + t of k_layer / v_layer.
+ * Positions >= max_ctx are skipped (the reference would write out of bounds). */
+int friday_attn_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
+                              const int* d_pos, int pos, int T, int head_dim, int num_q_heads, int num_kv_heads,
+                              int max_ctx, const float* rope_table, int neox, void* stream);
+
+/* int8 KV append: replaces storeKvQ8Kernel (cuda_math_kernels.cu:409-432, launched at
+ * transformer.cpp:1038-1040, 1233-1234). Per 32 values: dh = fp16(amax / 127),
+ * q = clamp(rne(x / dh), +-127). */
+int friday_attn_store_kv_q8(const uint16_t* k, const uint16_t* v, int8_t* k_layer, uint16_t* k_scale,
+                            int8_t* v_layer, uint16_t* v_scale, const int* d_pos, int pos, int T, int kv_dim,
+                            int max_ctx, void* stream);
+
+/* ---------------- decode attention ----------------
+ * friday_attn::launchDecodeAttention (attention_kernels.h:18-20, .cu:415-428):
+ * single-query GQA attention over positions [0, seq_len). Needs no workspace. */
+int friday_attn_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                                 int seq_len, int num_heads, int num_kv_heads, int head_dim, void* stream);
+/* friday_attn::launchDecodeAttentionDevPos (attention_kernels.h:24-25, .cu:430-442):
+ * sequence length *d_pos + 1, read on the device; max_seq_len bounds it. */
+int friday_attn_decode_attention_dev_pos(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                         uint16_t* out, const int* d_pos, int max_seq_len, int num_heads,
+                                         int num_kv_heads, int head_dim, void* stream);
+/* friday_attn::decodeAttentionFitsSharedMemory (attention_kernels.h:26, .cu:488-490).
+ * The LDS use here does not grow with the context: 1 for every max_seq_len > 0. */
+int friday_attn_decode_fits_shared_memory(int max_seq_len);
+/* friday_attn::splitAttentionWorkspaceBytes (attention_kernels.h:32, .cu:444-447):
+ * bytes of workspace for friday_attn_decode_attention_split, any head_dim <= 128. */
+size_t friday_attn_split_workspace_bytes(int num_heads, int max_seq_len);
+/* friday_attn::launchDecodeAttentionSplit (attention_kernels.h:35-38, .cu:449-486):
+ * split-K (flash-decoding) attention + LSE merge. Length = d_pos ? *d_pos + 1 : seq_len.
+ * k_scale/v_scale non-NULL: int8 caches with fp16 scales per 32 values. */
+int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out,
+                                       int seq_len, const int* d_pos, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                       void* stream, const uint16_t* k_scale, const uint16_t* v_scale);
+
+/* ---------------- prefill attention ----------------
+ * friday_attn::prefillAttentionSupported / launchPrefillAttention
+ * (attention_kernels.h:46-50, .cu:649-684): causal attention of T queries at
+ * positions *d_pos0 + t over cache positions [0, *d_pos0 + t] (the T new rows are
+ * already appended). q/out [T][num_heads*head_dim]. Runs on gfx950 MFMA.
+ * Returns 1 / 0 for supported / unsupported. */
+int friday_attn_prefill_supported(int num_heads, int num_kv_heads, int head_dim);
+int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out, int T,
+                                  const int* d_pos0, int num_heads, int num_kv_heads, int head_dim, void* stream,
+                                  const uint16_t* k_scale, const uint16_t* v_scale);
+
+/* ---------------- paged multi-sequence decode ----------------
+ * Semantics of the (unbuilt) experimental paged cache: 16-token pages, physical
+ * page = block_table[seq * block_table_stride + pos / 16], row pos % 16
+ * (experimental/runtime/src/kernels/paged_attention.cu:18-45, paged_kv_cache.h:16).
+ * seq_lens[b] = context length of sequence b AFTER its append (device int32).
+ * Every sequence gives the same result, bit for bit, as the contiguous-cache
+ * friday_attn_decode_attention_split over the same logical rows. */
+size_t friday_attn_paged_workspace_bytes(int batch, int num_heads, int max_seq_len);
+/* Append one token per sequence at position seq_lens[b] - 1 (RoPE as above).
+ * q [B][Hq*d], k/v [B][Hkv*d] rotated in place. */
+int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_pool, uint16_t* v_pool,
+                                    const int32_t* block_table, int block_table_stride, const int32_t* seq_lens,
+                                    int batch, int head_dim, int num_q_heads, int num_kv_heads, int max_ctx,
+                                    const float* rope_table, int neox, void* stream);
+int friday_attn_paged_decode_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                                       uint16_t* out, const int32_t* block_table, int block_table_stride,
+                                       const int32_t* seq_lens, int batch, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FRIDAY_ATTN_H */

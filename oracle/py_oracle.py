@@ -1,0 +1,181 @@
+"""ctypes bindings of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Loaded by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+The product library never imports this module.
+
+  Oracle   -> oracle/lib/libfa_oracle.so      (C restatement, fa_oracle.c)
+  RefCpu   -> oracle/_ref/libfriday_cpu_ref.so (reference cpu_ops.cpp et al.,
+              compiled from the reference sources; absent on machines without
+              /root/reference at build time)
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "lib", "libfa_oracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libfriday_cpu_ref.so")
+
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i = C.c_int
+
+
+def _f16bits(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        return a.view(np.uint16)
+    assert a.dtype == np.uint16, a.dtype
+    return a
+
+
+class Oracle:
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = C.CDLL(path)
+        L.or_half_to_float.restype = C.c_float
+        L.or_half_to_float.argtypes = [C.c_uint16]
+        L.or_float_to_half.restype = C.c_uint16
+        L.or_float_to_half.argtypes = [C.c_float]
+        L.or_round_to_half.restype = C.c_float
+        L.or_round_to_half.argtypes = [C.c_float]
+        L.or_halves_to_floats.argtypes = [_u16p, _f32p, C.c_size_t]
+        L.or_floats_to_halves.argtypes = [_f32p, _u16p, C.c_size_t]
+        L.or_rope_table.argtypes = [_f32p, _i, _i, C.c_float, C.c_void_p]
+        L.or_rope_append.argtypes = [_u16p, _u16p, _u16p, C.c_void_p, C.c_void_p, _f32p, _i, _i, _i, _i, _i, _i]
+        L.or_store_kv_q8.argtypes = [_u16p, _u16p, _i8p, _u16p, _i8p, _u16p, _i, _i, _i]
+        L.or_decode_attention.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
+        L.or_decode_attention_q8.argtypes = [_u16p, _i8p, _u16p, _i8p, _u16p, _f32p, _i, _i, _i, _i]
+        L.or_decode_attention_f64.argtypes = [_u16p, _u16p, _u16p, _f64p, _i, _i, _i, _i, _i]
+        L.or_decode_attention_split.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
+        L.or_lse_merge.argtypes = [_f32p, _f32p, _f32p, _i, _i, _f32p]
+        L.or_prefill_attention.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
+        L.or_prefill_attention_q8.argtypes = [_u16p, _i8p, _u16p, _i8p, _u16p, _f32p, _i, _i, _i, _i, _i]
+        L.or_paged_gather.argtypes = [_u16p, _i32p, _i, _i, _i, _u16p]
+
+    # fp16
+    def h2f(self, h) -> np.ndarray:
+        h = _f16bits(h)
+        out = np.empty(h.shape, np.float32)
+        self.lib.or_halves_to_floats(h.ravel(), out.ravel(), h.size)
+        return out
+
+    def f2h(self, f) -> np.ndarray:
+        f = np.ascontiguousarray(f, np.float32)
+        out = np.empty(f.shape, np.uint16)
+        self.lib.or_floats_to_halves(f.ravel(), out.ravel(), f.size)
+        return out
+
+    def round_to_half(self, x: float) -> float:
+        return self.lib.or_round_to_half(x)
+
+    # rope
+    def rope_table(self, max_pos, head_dim, base, freq_factors=None) -> np.ndarray:
+        cs = np.empty((max_pos, head_dim // 2, 2), np.float32)
+        ff = None
+        if freq_factors is not None:
+            ff = np.ascontiguousarray(freq_factors, np.float32)
+        self.lib.or_rope_table(cs.ravel(), max_pos, head_dim, base, None if ff is None else ff.ctypes.data)
+        return cs
+
+    def rope_append(self, q, k, v, k_cache, v_cache, cs, pos0, Hq, Hkv, d, neox):
+        """q [T][Hq*d], k/v [T][Hkv*d] uint16 (modified in place); caches [max_ctx][Hkv*d] or None."""
+        T = q.shape[0]
+        self.lib.or_rope_append(q, k, v, None if k_cache is None else k_cache.ctypes.data,
+                                None if v_cache is None else v_cache.ctypes.data, cs.ravel(), pos0, T, Hq, Hkv, d,
+                                int(neox))
+
+    def store_kv_q8(self, k, v, k8, ks, v8, vs, pos0, kv_dim):
+        T = k.shape[0]
+        self.lib.or_store_kv_q8(_f16bits(k), _f16bits(v), k8, ks, v8, vs, pos0, T, kv_dim)
+
+    # attention
+    def decode(self, q, kc, vc, S, Hq, Hkv, d, kv_stride=None) -> np.ndarray:
+        out = np.empty(Hq * d, np.float32)
+        self.lib.or_decode_attention(_f16bits(q).ravel(), _f16bits(kc).ravel(), _f16bits(vc).ravel(), out, S, Hq,
+                                     Hkv, d, kv_stride or Hkv * d)
+        return out
+
+    def decode_q8(self, q, k8, ks, v8, vs, S, Hq, Hkv, d) -> np.ndarray:
+        out = np.empty(Hq * d, np.float32)
+        self.lib.or_decode_attention_q8(_f16bits(q).ravel(), k8.ravel(), _f16bits(ks).ravel(), v8.ravel(),
+                                        _f16bits(vs).ravel(), out, S, Hq, Hkv, d)
+        return out
+
+    def decode_f64(self, q, kc, vc, S, Hq, Hkv, d) -> np.ndarray:
+        out = np.empty(Hq * d, np.float64)
+        self.lib.or_decode_attention_f64(_f16bits(q).ravel(), _f16bits(kc).ravel(), _f16bits(vc).ravel(), out, S,
+                                         Hq, Hkv, d, Hkv * d)
+        return out
+
+    def decode_split(self, q, kc, vc, S, Hq, Hkv, d, nsplit) -> np.ndarray:
+        out = np.empty(Hq * d, np.float32)
+        self.lib.or_decode_attention_split(_f16bits(q).ravel(), _f16bits(kc).ravel(), _f16bits(vc).ravel(), out, S,
+                                           Hq, Hkv, d, nsplit)
+        return out
+
+    def lse_merge(self, part_o, part_m, part_l) -> np.ndarray:
+        nsp, d = part_o.shape
+        out = np.empty(d, np.float32)
+        self.lib.or_lse_merge(np.ascontiguousarray(part_o, np.float32).ravel(),
+                              np.ascontiguousarray(part_m, np.float32), np.ascontiguousarray(part_l, np.float32),
+                              nsp, d, out)
+        return out
+
+    def prefill(self, q, kc, vc, T, p0, Hq, Hkv, d) -> np.ndarray:
+        out = np.empty((T, Hq * d), np.float32)
+        self.lib.or_prefill_attention(_f16bits(q).ravel(), _f16bits(kc).ravel(), _f16bits(vc).ravel(), out.ravel(),
+                                      T, p0, Hq, Hkv, d)
+        return out
+
+    def prefill_q8(self, q, k8, ks, v8, vs, T, p0, Hq, Hkv, d) -> np.ndarray:
+        out = np.empty((T, Hq * d), np.float32)
+        self.lib.or_prefill_attention_q8(_f16bits(q).ravel(), k8.ravel(), _f16bits(ks).ravel(), v8.ravel(),
+                                         _f16bits(vs).ravel(), out.ravel(), T, p0, Hq, Hkv, d)
+        return out
+
+    def paged_gather(self, pool, block_table, S, page, kv_dim) -> np.ndarray:
+        dst = np.empty((S, kv_dim), np.uint16)
+        self.lib.or_paged_gather(_f16bits(pool).ravel(), np.ascontiguousarray(block_table, np.int32), S, page,
+                                 kv_dim, dst.ravel())
+        return dst
+
+
+class RefCpu:
+    """The reference's own CPU functions (cpu_ops.cpp), compiled from source."""
+
+    def __init__(self, path: str = REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        L.ref_half_to_float.restype = C.c_float
+        L.ref_half_to_float.argtypes = [C.c_uint16]
+        L.ref_float_to_half.restype = C.c_uint16
+        L.ref_float_to_half.argtypes = [C.c_float]
+        L.ref_round_to_half.argtypes = [_f32p, _i]
+        L.ref_rope.argtypes = [_f32p, _f32p, _i, _i, _i, _i, C.c_float, _i, C.c_void_p]
+        L.ref_decode_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _i]
+        L.ref_pool_size.restype = _i
+        L.ref_pool_size.argtypes = [_i]
+
+    def rope(self, q, k, head_dim, nq, nk, pos, base, neox, freq_factors=None):
+        ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+        self.lib.ref_rope(q, k, head_dim, nq, nk, pos, base, int(neox), None if ff is None else ff.ctypes.data)
+
+    def decode(self, q, kc, vc, seq, Hq, Hkv, d, threads=1) -> np.ndarray:
+        out = np.empty(Hq * d, np.float32)
+        self.lib.ref_decode_attention(np.ascontiguousarray(q, np.float32).ravel(),
+                                      np.ascontiguousarray(kc, np.float32).ravel(),
+                                      np.ascontiguousarray(vc, np.float32).ravel(), out, seq, Hq, Hkv, d, threads)
+        return out
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)

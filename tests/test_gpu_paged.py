@@ -1,0 +1,110 @@
+"""GPU parity of paged multi-sequence append + decode.
+
+16-token pages with physical ids from a seeded permutation, one block table row
+per sequence. Bar: every sequence bit-identical to the contiguous-cache split
+decode over the same logical rows, and within tolerance of the CPU oracle.
+"""
+import numpy as np
+import pytest
+
+from fa_helpers import as_f32, assert_close, f16
+
+pytestmark = pytest.mark.gpu
+PAGE = 16
+
+
+def build_paged(rng, lens, kv_dim, max_seq):
+    """Contiguous per-sequence rows and the same rows scattered into a page pool."""
+    max_blocks = (max_seq + PAGE - 1) // PAGE
+    nblocks = [(s + PAGE - 1) // PAGE for s in lens]
+    total = sum(nblocks)
+    perm = rng.permutation(total).astype(np.int32)
+    table = np.full((len(lens), max_blocks), -1, np.int32)
+    k_pool = np.zeros((total, PAGE, kv_dim), np.uint16)
+    v_pool = np.zeros_like(k_pool)
+    seqs = []
+    at = 0
+    for b, s in enumerate(lens):
+        kc, vc = f16(rng, (s, kv_dim)), f16(rng, (s, kv_dim))
+        seqs.append((kc, vc))
+        for j in range(nblocks[b]):
+            phys = perm[at]
+            at += 1
+            table[b, j] = phys
+            rows = slice(j * PAGE, min(s, (j + 1) * PAGE))
+            n = rows.stop - rows.start
+            k_pool[phys, :n] = kc[rows]
+            v_pool[phys, :n] = vc[rows]
+    return seqs, table, k_pool, v_pool
+
+
+def contiguous_decode(fa, q, kc, vc, S, Hq, Hkv, d, max_seq):
+    dq, dk, dv = (fa.DeviceBuffer.from_array(a) for a in (q, kc, vc))
+    out = fa.DeviceBuffer(q.nbytes)
+    ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_seq))
+    dpos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
+    fa.launchDecodeAttentionSplit(dq, dk, dv, out, 0, dpos, max_seq, Hq, Hkv, d, ws)
+    fa.Hip.sync()
+    return out.download(q.size, np.uint16)
+
+
+@pytest.mark.parametrize("nseq,lo,hi,Hq,Hkv,d", [(6, 1, 3000, 40, 8, 128), (16, 256, 4096, 40, 8, 128),
+                                                 (5, 17, 700, 14, 2, 64)])
+def test_paged_matches_contiguous(gpu, oracle, nseq, lo, hi, Hq, Hkv, d):
+    fa = gpu
+    rng = np.random.default_rng(nseq * 1000 + hi)
+    kv_dim = Hkv * d
+    lens = [int(x) for x in rng.integers(lo, hi + 1, nseq)]
+    max_seq = max(lens) + 5
+    seqs, table, k_pool, v_pool = build_paged(rng, lens, kv_dim, max_seq)
+    q = f16(rng, (nseq, Hq * d))
+    dq = fa.DeviceBuffer.from_array(q)
+    dk, dv = fa.DeviceBuffer.from_array(k_pool), fa.DeviceBuffer.from_array(v_pool)
+    dt = fa.DeviceBuffer.from_array(table)
+    dl = fa.DeviceBuffer.from_array(np.array(lens, np.int32))
+    out = fa.DeviceBuffer(q.nbytes)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(nseq, Hq, max_seq))
+    fa.launchPagedDecodeAttention(dq, dk, dv, out, dt, table.shape[1], dl, nseq, max_seq, Hq, Hkv, d, ws)
+    fa.Hip.sync()
+    got = out.download((nseq, Hq * d), np.uint16)
+    for b, S in enumerate(lens):
+        kc, vc = seqs[b]
+        cont = contiguous_decode(fa, q[b], kc, vc, S, Hq, Hkv, d, max_seq)
+        assert np.array_equal(got[b], cont), f"seq {b} (S={S}) differs from the contiguous result"
+        assert_close(as_f32(got[b]), oracle.decode(q[b], kc, vc, S, Hq, Hkv, d), f"seq {b} S={S}")
+
+
+def test_paged_append_then_decode(gpu, oracle):
+    """Append one token per sequence through the block table, then decode; caches bit-exact."""
+    fa = gpu
+    Hq, Hkv, d, nseq = 40, 8, 128, 7
+    kv_dim = Hkv * d
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(1, 900, nseq)]   # lengths AFTER the append
+    max_seq = 1024
+    seqs, table, k_pool, v_pool = build_paged(rng, lens, kv_dim, max_seq)
+    q = f16(rng, (nseq, Hq * d))
+    k = f16(rng, (nseq, kv_dim))
+    v = f16(rng, (nseq, kv_dim))
+    rope = fa.rope_table_host(max_seq, d, 1e6)
+    bufs = {n: fa.DeviceBuffer.from_array(a) for n, a in
+            dict(q=q, k=k, v=v, kp=k_pool, vp=v_pool, t=table, l=np.array(lens, np.int32), r=rope).items()}
+    fa.pagedRopeStoreKv(bufs["q"], bufs["k"], bufs["v"], bufs["kp"], bufs["vp"], bufs["t"], table.shape[1],
+                        bufs["l"], nseq, d, Hq, Hkv, max_seq, bufs["r"], 1)
+    out = fa.DeviceBuffer(q.nbytes)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(nseq, Hq, max_seq))
+    fa.launchPagedDecodeAttention(bufs["q"], bufs["kp"], bufs["vp"], out, bufs["t"], table.shape[1], bufs["l"],
+                                  nseq, max_seq, Hq, Hkv, d, ws)
+    fa.Hip.sync()
+    got_kp = bufs["kp"].download(k_pool.shape, np.uint16)
+    got_vp = bufs["vp"].download(v_pool.shape, np.uint16)
+    got = as_f32(out.download((nseq, Hq * d), np.uint16))
+    for b, S in enumerate(lens):
+        kc, vc = seqs[b]
+        qb, kb = q[b:b + 1].copy(), k[b:b + 1].copy()
+        oracle.rope_append(qb, kb, v[b:b + 1], kc, vc, rope, S - 1, Hq, Hkv, d, 1)
+        pos = S - 1
+        phys = table[b, pos // PAGE]
+        assert np.array_equal(got_kp[phys, pos % PAGE], kc[pos]), f"k row seq {b}"
+        assert np.array_equal(got_vp[phys, pos % PAGE], vc[pos]), f"v row seq {b}"
+        assert_close(got[b], oracle.decode(qb[0], kc, vc, S, Hq, Hkv, d), f"paged seq {b}")
