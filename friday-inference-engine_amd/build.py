@@ -19,6 +19,9 @@ OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libfriday_attn.so")
 SOURCES = ["fa_api.cpp", "fa_append.hip", "fa_decode.hip", "fa_prefill.hip"]
+# benchmark-only helpers (synthetic fill, calibration copy), a separate library
+BENCHKIT_SOURCES = ["fa_benchkit.hip"]
+BENCHKIT = os.path.join(LIB_DIR, "libfa_benchkit.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -38,24 +41,33 @@ def _run(cmd):
     return out
 
 
+def _compile(sources, ex):
+    objs, jobs = [], []
+    for src in sources:
+        obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+        objs.append(obj)
+        jobs.append(ex.submit(_run, [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]))
+    return objs, jobs
+
+
+def _link(objs, target):
+    tmp = target + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, target)
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
-    objs = []
-    jobs = []
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        for src in SOURCES:
-            obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-            objs.append(obj)
-            cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
-            jobs.append(ex.submit(_run, cmd))
-        for j in jobs:
+    with cf.ThreadPoolExecutor(max_workers=8) as ex:
+        objs, jobs = _compile(SOURCES, ex)
+        bobjs, bjobs = _compile(BENCHKIT_SOURCES, ex)
+        for j in jobs + bjobs:
             out = j.result()
             if verbose and out.strip():
                 print(out)
-    tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
+    _link(objs, LIB)
+    _link(bobjs, BENCHKIT)
     return LIB
 
 

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -65,12 +66,54 @@ void rope_fill(float* table, int max_ctx, int head_dim, float freq_base, const f
     }
 }
 
+int env_int(const char* name, int dflt, int lo, int hi) {
+    const char* e = std::getenv(name);
+    if (!e || !*e) return dflt;
+    const int v = std::atoi(e);
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// Workspace: counters [B*Hq] int at offset 0 (the fused merge uses
+// B*Hkv*ceil(G/16) <= B*Hq of them; they must stay at a fixed place whatever the
+// split count of a call), then part_o [B*Hq][ns][d] fp32 and part_ml [B*Hq][ns][2].
+size_t counters_bytes(int batch, int Hq) { return ((size_t)batch * Hq * sizeof(int) + 255) / 256 * 256; }
+
 size_t split_ws_bytes(int batch, int Hq, int max_seq, int d) {
-    const size_t ns = (size_t)fa::split_count(max_seq);
-    return (size_t)batch * Hq * ns * ((size_t)d + 2) * sizeof(float);
+    const size_t ns = (size_t)fa::split_bound(max_seq, fa::min_chunk(), fa::max_splits());
+    return counters_bytes(batch, Hq) + (size_t)batch * Hq * ns * ((size_t)d + 2) * sizeof(float);
+}
+
+void set_workspace(fa::DecodeParams& p, void* ws, int batch, int d, bool fused) {
+    char* base = static_cast<char*>(ws);
+    p.counters = fused ? reinterpret_cast<int*>(base) : nullptr;
+    p.part_o = reinterpret_cast<float*>(base + counters_bytes(batch, p.Hq));
+    p.part_ml = p.part_o + (size_t)batch * p.Hq * p.nsplit_grid * d;
 }
 
 }  // namespace
+
+namespace fa {
+// Split partition: about S / min_chunk splits of >= min_chunk positions, at most
+// max_splits (a multiple of 128 and <= 256 respectively).
+int min_chunk() {
+    static const int v = env_int("FRIDAY_ATTN_MIN_CHUNK", 256, 1, 1 << 20) / kSpan * kSpan;
+    return v < kSpan ? kSpan : v;
+}
+int max_splits() {
+    static const int v = env_int("FRIDAY_ATTN_MAX_SPLITS", kMaxSplitsLimit, 1, kMaxSplitsLimit);
+    return v;
+}
+// Splits per (kv head, head block) so that one sequence keeps about `target`
+// workgroups streaming: one per CU of the MI355X (256). The partition stays a
+// function of S and the head layout only, never of the batch.
+int splits_for(int Hkv, int ngb) {
+    static const int target = env_int("FRIDAY_ATTN_TARGET_WGS", 256, 1, 1 << 16);
+    const int groups = Hkv * ngb;
+    int ns = target / (groups > 0 ? groups : 1);
+    ns = ns < 1 ? 1 : ns;
+    return ns < max_splits() ? ns : max_splits();
+}
+}  // namespace fa
 
 extern "C" {
 
@@ -144,7 +187,7 @@ int friday_attn_store_kv_q8(const uint16_t* k, const uint16_t* v, int8_t* k_laye
 
 static int decode_common(const char* w, const uint16_t* q, const void* k, const void* v, uint16_t* out, int seq_len,
                          const int* d_pos, int max_seq, int Hq, int Hkv, int d, void* ws, size_t ws_bytes,
-                         bool single, const uint16_t* ks, const uint16_t* vs, void* stream) {
+                         bool single, bool fused, const uint16_t* ks, const uint16_t* vs, void* stream) {
     if (int rc = check_heads(w, Hq, Hkv, d)) return rc;
     if (!q || !k || !v || !out) return fail(FA_ERR_INVALID, "%s: null tensor", w);
     if (max_seq <= 0) return fail(FA_ERR_INVALID, "%s: invalid max_seq_len %d", w, max_seq);
@@ -159,16 +202,17 @@ static int decode_common(const char* w, const uint16_t* q, const void* k, const 
     p.max_seq = max_seq;
     p.out = out; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.ngb = (G + 15) / 16; p.kv_dim = Hkv * d;
     p.single = single ? 1 : 0;
+    p.min_chunk = fa::min_chunk();
+    p.max_splits = fa::splits_for(Hkv, p.ngb);
     p.scale2 = (1.0f / std::sqrt((float)d)) * 1.4426950408889634f;
     if (!single) {
         // host length: the grid only needs the splits of seq_len
         const int grid_len = d_pos ? max_seq : seq_len;
-        p.nsplit_grid = fa::split_count(grid_len);
+        p.nsplit_grid = fa::split_bound(grid_len, p.min_chunk, p.max_splits);
         const size_t need = split_ws_bytes(1, Hq, grid_len, d);
         if (!ws || ws_bytes < need)
             return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, ws_bytes);
-        p.part_o = static_cast<float*>(ws);
-        p.part_ml = p.part_o + (size_t)Hq * p.nsplit_grid * d;
+        set_workspace(p, ws, 1, d, fused);
     } else {
         p.nsplit_grid = 1;
     }
@@ -178,7 +222,7 @@ static int decode_common(const char* w, const uint16_t* q, const void* k, const 
 int friday_attn_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
                                  int seq_len, int num_heads, int num_kv_heads, int head_dim, void* stream) {
     return decode_common("decode_attention", q, k_cache, v_cache, out, seq_len, nullptr, seq_len > 0 ? seq_len : 1,
-                         num_heads, num_kv_heads, head_dim, nullptr, 0, true, nullptr, nullptr, stream);
+                         num_heads, num_kv_heads, head_dim, nullptr, 0, true, false, nullptr, nullptr, stream);
 }
 
 int friday_attn_decode_attention_dev_pos(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -186,7 +230,7 @@ int friday_attn_decode_attention_dev_pos(const uint16_t* q, const uint16_t* k_ca
                                          int num_kv_heads, int head_dim, void* stream) {
     if (!d_pos) return fail(FA_ERR_INVALID, "decode_attention_dev_pos: d_pos is null");
     return decode_common("decode_attention_dev_pos", q, k_cache, v_cache, out, 0, d_pos, max_seq_len, num_heads,
-                         num_kv_heads, head_dim, nullptr, 0, true, nullptr, nullptr, stream);
+                         num_kv_heads, head_dim, nullptr, 0, true, false, nullptr, nullptr, stream);
 }
 
 int friday_attn_decode_fits_shared_memory(int max_seq_len) { return max_seq_len > 0 ? 1 : 0; }
@@ -201,7 +245,50 @@ int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, c
                                        int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
                                        void* stream, const uint16_t* k_scale, const uint16_t* v_scale) {
     return decode_common("decode_attention_split", q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads,
-                         num_kv_heads, head_dim, workspace, workspace_bytes, false, k_scale, v_scale, stream);
+                         num_kv_heads, head_dim, workspace, workspace_bytes, false, false, k_scale, v_scale, stream);
+}
+
+int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+    if (!workspace || workspace_bytes == 0 || workspace_bytes % 4)
+        return fail(FA_ERR_INVALID, "decode_workspace_init: invalid workspace");
+    return launch_status(fa::launch_zero_fill(workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
+                         "decode_workspace_init");
+}
+
+int friday_attn_decode_attention_fused(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out,
+                                       int seq_len, const int* d_pos, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                       void* stream, const uint16_t* k_scale, const uint16_t* v_scale) {
+    return decode_common("decode_attention_fused", q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads,
+                         num_kv_heads, head_dim, workspace, workspace_bytes, false, true, k_scale, v_scale, stream);
+}
+
+int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
+                            uint16_t* out, const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,
+                            int head_dim, const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    const char* w = "decode_step";
+    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
+    if (!q || !k || !v || !k_layer || !v_layer || !out || !rope_table || max_ctx <= 0)
+        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if (!d_pos && (pos < 0 || pos >= max_ctx))
+        return fail(FA_ERR_INVALID, "%s: position %d outside [0, %d)", w, pos, max_ctx);
+    const int G = num_heads / num_kv_heads;
+    fa::DecodeParams p{};
+    p.q = q; p.k = k_layer; p.v = v_layer; p.d_pos = d_pos; p.seq_len = d_pos ? 0 : pos + 1; p.max_seq = max_ctx;
+    p.out = out; p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = G; p.ngb = (G + 15) / 16;
+    p.kv_dim = num_kv_heads * head_dim;
+    p.min_chunk = fa::min_chunk();
+    p.max_splits = fa::splits_for(num_kv_heads, p.ngb);
+    p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
+    p.rope_table = rope_table; p.k_new = k; p.v_new = v; p.neox = neox ? 1 : 0;
+    const int grid_len = d_pos ? max_ctx : pos + 1;
+    p.nsplit_grid = fa::split_bound(grid_len, p.min_chunk, p.max_splits);
+    const size_t need = split_ws_bytes(1, num_heads, grid_len, head_dim);
+    if (!workspace || workspace_bytes < need)
+        return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
+    set_workspace(p, workspace, 1, head_dim, true);
+    return launch_status(fa::launch_decode(p, head_dim, 1, false, false, static_cast<hipStream_t>(stream)), w);
 }
 
 // ---------------- prefill ----------------
@@ -227,6 +314,34 @@ int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const 
 
 // ---------------- paged ----------------
 
+static int paged_decode_common(const char* w, uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                               uint16_t* k_pool, uint16_t* v_pool, uint16_t* out, const int32_t* block_table,
+                               int block_table_stride, const int32_t* seq_lens, int batch, int max_seq_len,
+                               int num_heads, int num_kv_heads, int head_dim, const float* rope_table, int neox,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
+    if (batch <= 0 || max_seq_len <= 0 || !q || !k_pool || !v_pool || !out || !block_table || !seq_lens)
+        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if ((long long)block_table_stride * FA_PAGE_TOKENS < max_seq_len)
+        return fail(FA_ERR_INVALID, "%s: block_table_stride %d cannot address max_seq_len %d", w,
+                    block_table_stride, max_seq_len);
+    const int G = num_heads / num_kv_heads;
+    fa::DecodeParams p{};
+    p.q = q; p.k = k_pool; p.v = v_pool; p.block_table = block_table; p.bt_stride = block_table_stride;
+    p.seq_lens = seq_lens; p.max_seq = max_seq_len; p.out = out;
+    p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = G; p.ngb = (G + 15) / 16; p.kv_dim = num_kv_heads * head_dim;
+    p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
+    p.rope_table = rope_table; p.k_new = k_new; p.v_new = v_new; p.neox = neox ? 1 : 0;
+    p.min_chunk = fa::min_chunk();
+    p.max_splits = fa::splits_for(num_kv_heads, p.ngb);
+    p.nsplit_grid = fa::split_bound(max_seq_len, p.min_chunk, p.max_splits);
+    const size_t need = split_ws_bytes(batch, num_heads, max_seq_len, head_dim);
+    if (!workspace || workspace_bytes < need)
+        return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
+    set_workspace(p, workspace, batch, head_dim, true);
+    return launch_status(fa::launch_decode(p, head_dim, batch, true, false, static_cast<hipStream_t>(stream)), w);
+}
+
 size_t friday_attn_paged_workspace_bytes(int batch, int num_heads, int max_seq_len) {
     if (batch <= 0 || num_heads <= 0 || max_seq_len <= 0) return 0;
     return split_ws_bytes(batch, num_heads, max_seq_len, 128);
@@ -249,31 +364,27 @@ int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v,
     return launch_status(fa::launch_rope_store(p, true, static_cast<hipStream_t>(stream)), w);
 }
 
+int friday_attn_paged_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_pool,
+                                  uint16_t* v_pool, uint16_t* out, const int32_t* block_table,
+                                  int block_table_stride, const int32_t* seq_lens, int batch, int max_seq_len,
+                                  int num_heads, int num_kv_heads, int head_dim, const float* rope_table, int neox,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    const char* w = "paged_decode_step";
+    if (!k || !v || !rope_table) return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    return paged_decode_common(w, q, k, v, k_pool, v_pool, out, block_table, block_table_stride, seq_lens, batch,
+                               max_seq_len, num_heads, num_kv_heads, head_dim, rope_table, neox, workspace,
+                               workspace_bytes, stream);
+}
+
 int friday_attn_paged_decode_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                                        uint16_t* out, const int32_t* block_table, int block_table_stride,
                                        const int32_t* seq_lens, int batch, int max_seq_len, int num_heads,
                                        int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
                                        void* stream) {
-    const char* w = "paged_decode_attention";
-    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
-    if (batch <= 0 || max_seq_len <= 0 || !q || !k_pool || !v_pool || !out || !block_table || !seq_lens)
-        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
-    if ((long long)block_table_stride * FA_PAGE_TOKENS < max_seq_len)
-        return fail(FA_ERR_INVALID, "%s: block_table_stride %d cannot address max_seq_len %d", w,
-                    block_table_stride, max_seq_len);
-    const int G = num_heads / num_kv_heads;
-    fa::DecodeParams p{};
-    p.q = q; p.k = k_pool; p.v = v_pool; p.block_table = block_table; p.bt_stride = block_table_stride;
-    p.seq_lens = seq_lens; p.max_seq = max_seq_len; p.out = out;
-    p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = G; p.ngb = (G + 15) / 16; p.kv_dim = num_kv_heads * head_dim;
-    p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
-    p.nsplit_grid = fa::split_count(max_seq_len);
-    const size_t need = split_ws_bytes(batch, num_heads, max_seq_len, head_dim);
-    if (!workspace || workspace_bytes < need)
-        return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
-    p.part_o = static_cast<float*>(workspace);
-    p.part_ml = p.part_o + (size_t)batch * num_heads * p.nsplit_grid * head_dim;
-    return launch_status(fa::launch_decode(p, head_dim, batch, true, false, static_cast<hipStream_t>(stream)), w);
+    return paged_decode_common("paged_decode_attention", const_cast<uint16_t*>(q), nullptr, nullptr,
+                               const_cast<uint16_t*>(k_pool), const_cast<uint16_t*>(v_pool), out, block_table,
+                               block_table_stride, seq_lens, batch, max_seq_len, num_heads, num_kv_heads, head_dim,
+                               nullptr, 0, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -5,24 +5,18 @@
 // Rotation (cpu_ops.cpp:26-43, cuda_math_kernels.cu:363-404):
 //   x0' = x0*c - x1*s, x1' = x0*s + x1*c in fp32, NaN -> 0, clamp +-65504, RNE fp16;
 //   neox pairs (i, i + d/2), otherwise (2i, 2i + 1).
-// (c, s) come from the host-built table (fa_rope_table.cpp) and the products are
-// not contracted into FMAs, so the stored bits equal the reference CPU path's.
+// (c, s) come from the host-built table (friday_attn_rope_table_*) and the products
+// are not contracted into FMAs, so the stored bits equal the reference CPU path's.
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
 namespace fa {
 namespace {
 
-__device__ __forceinline__ float rot_clamp(float r) {
-    if (__builtin_isnan(r)) return 0.0f;
-    return fminf(fmaxf(r, -65504.0f), 65504.0f);
-}
-
 // One thread per (token, head, rotation pair). Heads [0, Hq) are query heads,
 // [Hq, Hq + Hkv) key heads (their thread also moves the matching v pair).
 template <bool PAGED>
 __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
-#pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int hd2 = p.D >> 1;
     const int idx = blockIdx.x * 256 + threadIdx.x;
@@ -37,10 +31,8 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
     const bool is_k = h >= p.Hq;
     _Float16* x = is_k ? reinterpret_cast<_Float16*>(p.k) + (size_t)t * kv_dim + (h - p.Hq) * p.D
                        : reinterpret_cast<_Float16*>(p.q) + (size_t)t * p.Hq * p.D + h * p.D;
-    const float a = (float)x[o0], b = (float)x[o1];
-    const float ac = a * cs.x, bs = b * cs.y, as = a * cs.y, bc = b * cs.x;
-    const _Float16 r0 = (_Float16)rot_clamp(ac - bs);
-    const _Float16 r1 = (_Float16)rot_clamp(as + bc);
+    _Float16 r0, r1;
+    rope_rotate((float)x[o0], (float)x[o1], cs.x, cs.y, r0, r1);
     x[o0] = r0;
     x[o1] = r1;
     if (is_k && p.k_dst) {

@@ -24,7 +24,46 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// D = A(16x16) * B(16x16) + C: lane l holds row/column l%16 of A/B and 4
+// consecutive k values of block l/16; C/D as above.
+__device__ __forceinline__ f4 mfma16x16x16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives in slot k
+// element (i % 4) of the four fp16 values addressed by lane 4k + i/4 of its group.
+__device__ __forceinline__ h4 lds_read_tr16(const unsigned char* p) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    const s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4*)(__attribute__((address_space(3))) const void*)p);
+    return *reinterpret_cast<const h4*>(&r);
+}
+
+// A operand of O^T = V^T P^T from a row-major fp16 V tile (row stride `ldr` bytes)
+// for MFMA k-slots j = 0..3 -> tile rows kb*4 + j and j = 4..7 -> rows 16 + kb*4 + j-4,
+// column (output dim) = lane % 16 of the 16-wide d tile. `p` must point at row
+// kb*4 + (lane%16)/4, column d0 + 4*(lane % 4) of the lane's group kb = lane / 16.
+__device__ __forceinline__ h8 read_vt(const unsigned char* p, int ldr) {
+    const h4 lo = lds_read_tr16(p);
+    const h4 hi = lds_read_tr16(p + 16 * ldr);
+    return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// One RoPE rotation (cpu_ops.cpp:37-40, cuda_math_kernels.cu:387-392):
+// x0' = x0*c - x1*s, x1' = x0*s + x1*c with every product rounded on its own
+// (no FMA contraction), then NaN -> 0, clamp to +-65504, RNE fp16.
+__device__ __forceinline__ float rot_clamp(float r) {
+    if (__builtin_isnan(r)) return 0.0f;
+    return fminf(fmaxf(r, -65504.0f), 65504.0f);
+}
+__device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, _Float16& r0, _Float16& r1) {
+#pragma clang fp contract(off)
+    const float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+    r0 = (_Float16)rot_clamp(ac - bs);
+    r1 = (_Float16)rot_clamp(as + bc);
+}
 
 // Reference output rule: NaN -> 0, clamp to +-65504, round to nearest even fp16.
 __device__ __forceinline__ _Float16 out_half(float r) {
@@ -35,6 +74,38 @@ __device__ __forceinline__ _Float16 out_half(float r) {
 
 __device__ __forceinline__ float wave_max_xor(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
 __device__ __forceinline__ float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+
+// Agent-scope coherent access (global_store/load ... sc1): the store is written
+// through to the device coherence point and the load bypasses a possibly stale
+// XCD-local L2 line, so data handed between workgroups of one launch needs no
+// cache-wide buffer_wbl2 / buffer_inv fence.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Agent-coherent buffer loads (cache policy sc1): they see data that other
+// workgroups of the same launch wrote through to memory, without a cache-wide
+// invalidate, and unlike volatile accesses they pipeline like ordinary loads.
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
+constexpr int kCpolSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ f4 ld_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const i4v x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCpolSc1);
+    return *reinterpret_cast<const f4*>(&x);
+}
+__device__ __forceinline__ float2 ld_coherent2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const i2v x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, kCpolSc1);
+    return *reinterpret_cast<const float2*>(&x);
+}
+
+// s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
+// The memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <typename T>
 __device__ __forceinline__ T ld_nt(const T* p) {

@@ -25,7 +25,11 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kTile = 32;
+constexpr int kTile = 16;  // positions per wave tile
+#ifndef FA_DECODE_STAGES
+#define FA_DECODE_STAGES 1
+#endif
+constexpr int kStages = FA_DECODE_STAGES;  // register stages (tiles in flight) per wave
 
 template <int D, bool Q8>
 struct Geo {
@@ -39,7 +43,9 @@ struct Geo {
     static constexpr int NLD = kTile / RPI;           // loads per tile per tensor
     static constexpr int WAVE_LDS = 2 * kTile * LROW;  // K and V tile of one wave
     static constexpr int COMB_LDS = kWaves * 16 * (D + 2) * 4;
-    static constexpr int LDS = (kWaves * WAVE_LDS > COMB_LDS ? kWaves * WAVE_LDS : COMB_LDS);
+    static constexpr int MERGE_LDS = (2 * (kThreads / (D / 4)) * 128 + 64) * 4;
+    static constexpr int LDS0 = (kWaves * WAVE_LDS > COMB_LDS ? kWaves * WAVE_LDS : COMB_LDS);
+    static constexpr int LDS = LDS0 > MERGE_LDS ? LDS0 : MERGE_LDS;
 };
 
 __device__ __forceinline__ int context_len(const DecodeParams& p, int b, bool paged) {
@@ -69,7 +75,108 @@ __device__ __forceinline__ void dequant16(u4 raw, float sc, u4& lo, u4& hi) {
     hi = *reinterpret_cast<u4*>(&b);
 }
 
-template <int D, bool PAGED, bool Q8>
+// Log-sum-exp merge of the split partials of nh consecutive query-head rows
+// (row0 .. row0+nh-1) by the 256 threads of a workgroup, one thread per output
+// float4: M = max m_s, w_s = exp(m_s - M) (0 below -50),
+// out = sum_s w_s o_s / sum_s w_s l_s, NaN -> 0, clamp, fp16
+// (attention_kernels.cu:207-235). The sums run over s in increasing order for
+// every head, so the merge kernel (nh = 1) and the fused last-workgroup merge
+// (nh = heads of the group) give the same bits. Partials are read with loads that
+// bypass the caches: in the fused path other workgroups of this launch wrote them
+// through to memory just before.
+constexpr int kMergeBatch = 32;  // partial rows loaded per round trip
+template <int D>
+__device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
+    constexpr int C4 = D / 4;
+    constexpr int HB = kThreads / C4;  // heads per pass
+    constexpr int K = kMaxSplitsLimit;
+    float* s_m = lds;            // [HB][K]  max of each split, then its weight
+    float* s_l = s_m + HB * K;   // [HB][K]  sum of each split, then weight * sum
+    float* s_L = s_l + HB * K;   // [HB]
+    const int tid = threadIdx.x;
+    const int hh = tid / C4, c = tid % C4;
+    const int npad = (nsp + 7) & ~7;  // padded entries: max -inf, sum 0 -> weight exactly 0
+    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(p.part_o + row0 * p.nsplit_grid * D, (uint32_t)(nh * p.nsplit_grid * D * 4));
+    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml + row0 * p.nsplit_grid * 2, (uint32_t)(nh * p.nsplit_grid * 8));
+    for (int h0 = 0; h0 < nh; h0 += HB) {
+        const int hn = min(HB, nh - h0);
+        const bool act = hh < hn;
+        const size_t orow = row0 + h0 + (act ? hh : 0);
+        const uint32_t obase = (uint32_t)(((h0 + (act ? hh : 0)) * p.nsplit_grid * D + 4 * c) * 4);
+        // first batch of this thread's partial columns, issued before the weights are known
+        f4 ov[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
+        for (int i = tid; i < hn * npad; i += kThreads) {
+            const int h = i / npad, sp = i - h * npad;
+            const float2 ml = ld_coherent2(rml, (uint32_t)(((h0 + h) * p.nsplit_grid + min(sp, nsp - 1)) * 8));
+            const float m = ml.x, l = ml.y;
+            s_m[h * K + sp] = sp < nsp ? m : -__builtin_inff();
+            s_l[h * K + sp] = sp < nsp ? l : 0.0f;
+        }
+        __syncthreads();
+        // one thread per (head, split): the head's max, then this split's weight
+        float wgt[(HB * K + kThreads - 1) / kThreads], wl[(HB * K + kThreads - 1) / kThreads];
+#pragma unroll
+        for (int r = 0; r < (HB * K + kThreads - 1) / kThreads; ++r) {
+            const int i = tid + r * kThreads;
+            wgt[r] = 0.0f;
+            wl[r] = 0.0f;
+            if (i < hn * npad) {
+                const int h = i / npad, sp = i - h * npad;
+                const float* m = s_m + h * K;
+                float M = -__builtin_inff();
+                for (int t = 0; t < npad; t += 8)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) M = fmaxf(M, m[t + k]);
+                const float df = m[sp] - M;
+                wgt[r] = df < kCut2 ? 0.0f : exp2_fast(df);
+                wl[r] = wgt[r] * s_l[h * K + sp];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < (HB * K + kThreads - 1) / kThreads; ++r) {
+            const int i = tid + r * kThreads;
+            if (i < hn * npad) {
+                const int h = i / npad, sp = i - h * npad;
+                s_m[h * K + sp] = wgt[r];
+                s_l[h * K + sp] = wl[r];
+            }
+        }
+        __syncthreads();
+        if (tid < hn) {  // L in a fixed order: eight interleaved partial sums, then a tree
+            const float* wlh = s_l + tid * K;
+            float Lp[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) Lp[k] = 0.0f;
+            for (int t = 0; t < npad; t += 8)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) Lp[k] += wlh[t + k];
+            s_L[tid] = ((Lp[0] + Lp[1]) + (Lp[2] + Lp[3])) + ((Lp[4] + Lp[5]) + (Lp[6] + Lp[7]));
+        }
+        __syncthreads();
+        if (act) {
+            const float* w = s_m + hh * K;
+            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j)
+                if (j < nsp) acc += w[j] * ov[j];
+            for (int sp = kMergeBatch; sp < nsp; ++sp) acc += w[sp] * ld_coherent4(ro, obase + (uint32_t)(sp * D * 4));
+            const float L = s_L[hh];
+            h4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
+            reinterpret_cast<h4*>(p.out + orow * D)[c] = o;
+        }
+        __syncthreads();  // LDS reused by the next pass
+    }
+}
+
+template <int D>
+constexpr int merge_lds_bytes() { return (2 * (kThreads / (D / 4)) * kMaxSplitsLimit + 64) * 4; }
+
+template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
 __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     using Gm = Geo<D, Q8>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
@@ -78,8 +185,9 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     const int kvh = blockIdx.y / p.ngb, gb = blockIdx.y % p.ngb;
     const int b = blockIdx.z;
     const int S = context_len(p, b, PAGED);
-    const int chunk = p.single ? (S > 0 ? ((S + kSpan - 1) / kSpan) * kSpan : kSpan) : split_chunk(S);
-    const int nsp = p.single ? 1 : split_count(S);
+    const int chunk = p.single ? (S > 0 ? ((S + kSpan - 1) / kSpan) * kSpan : kSpan)
+                               : split_chunk(S, p.min_chunk, p.max_splits);
+    const int nsp = p.single ? 1 : split_count(S, p.min_chunk, p.max_splits);
     if (split >= nsp) return;  // inactive split; the merge ignores it
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
@@ -101,6 +209,65 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         }
     }
 
+    int append_wave = -1, append_tile = -1;
+    if (ROPE && S > 0) {
+        // rotate this lane's q fragment at the new token's position S-1; both halves of
+        // every rotation pair sit in the same lane (neox: k-steps s and s + KSTEPS/2,
+        // interleaved: neighbouring elements of one fragment)
+        constexpr int HD2 = D / 2;
+        const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)(S - 1) * HD2;
+        if (p.neox) {
+#pragma unroll
+            for (int s = 0; s < Gm::KSTEPS / 2; ++s)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float2 c = cs[s * 32 + kb * 8 + j];
+                    _Float16 r0, r1;
+                    rope_rotate((float)qf[s][j], (float)qf[s + Gm::KSTEPS / 2][j], c.x, c.y, r0, r1);
+                    qf[s][j] = r0;
+                    qf[s + Gm::KSTEPS / 2][j] = r1;
+                }
+        } else {
+#pragma unroll
+            for (int s = 0; s < Gm::KSTEPS; ++s)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const float2 c = cs[(s * 32 + kb * 8 + j) / 2];
+                    _Float16 r0, r1;
+                    rope_rotate((float)qf[s][j], (float)qf[s][j + 1], c.x, c.y, r0, r1);
+                    qf[s][j] = r0;
+                    qf[s][j + 1] = r1;
+                }
+        }
+        if (!gvalid) {
+#pragma unroll
+            for (int s = 0; s < Gm::KSTEPS; ++s) qf[s] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        // the wave that will load the tile holding position S-1 (in the split holding it)
+        // writes the new row of this kv head; it waits for its own stores just before it
+        // issues that tile's loads (same wave, same L2: then the loads see the row)
+        const int s_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
+        const int last_tile = (end - start - 1) / kTile;
+        append_wave = (split == nsp - 1 && s_raw == S) ? last_tile % kWaves : -1;  // past max_seq: no append
+        append_tile = last_tile;
+        if (wave == append_wave && lane < HD2) {
+            const int o0 = p.neox ? lane : 2 * lane, o1 = p.neox ? lane + HD2 : 2 * lane + 1;
+            const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
+            const _Float16* kn = reinterpret_cast<const _Float16*>(p.k_new) + src;
+            const _Float16* vn = reinterpret_cast<const _Float16*>(p.v_new) + src;
+            const float2 c = cs[lane];
+            _Float16 r0, r1;
+            rope_rotate((float)kn[o0], (float)kn[o1], c.x, c.y, r0, r1);
+            const size_t dst = row_index<PAGED>(p, b, S - 1) * p.kv_dim + (size_t)kvh * D;
+            _Float16* kd = const_cast<_Float16*>(reinterpret_cast<const _Float16*>(p.k)) + dst;
+            _Float16* vd = const_cast<_Float16*>(reinterpret_cast<const _Float16*>(p.v)) + dst;
+            kd[o0] = r0;
+            kd[o1] = r1;
+            vd[o0] = vn[o0];
+            vd[o1] = vn[o1];
+        }
+    }
+
     unsigned char* kl = smem + wave * Gm::WAVE_LDS;
     unsigned char* vl = kl + kTile * Gm::LROW;
     const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * (Q8 ? D : D * 2);
@@ -112,111 +279,120 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < Gm::DTILES; ++i) o[i] = f4{0.f, 0.f, 0.f, 0.f};
 
+    // NST register stages per wave: while one 16-row tile is consumed, the next
+    // NST-1 tiles of this wave are already in flight. Loads are unconditional (rows past
+    // the end re-read the last valid row and are zeroed) so the wait counts stay
+    // static and never collapse to a full drain.
     const int ntiles = (end - start + kTile - 1) / kTile;
-    u4 kr[Gm::NLD], vr[Gm::NLD];
-    float ksc[Gm::NLD], vsc[Gm::NLD];
     const int lrow = lane / Gm::CPR, lchunk = lane % Gm::CPR;
+    struct Stage {
+        u4 k[Gm::NLD], v[Gm::NLD];
+        float ks[Gm::NLD], vs[Gm::NLD];
+    };
+    Stage st[NST];
 
-    auto load_tile = [&](int t) {
+    auto load_tile = [&](Stage& st, int t) {
+        if (ROPE && t == append_tile && wave == append_wave) wait_vmem();  // the appended row is stored
         const int base = start + t * kTile;
 #pragma unroll
         for (int r = 0; r < Gm::NLD; ++r) {
             const int pos = base + r * Gm::RPI + lrow;
-            if (pos < end) {
-                const size_t ri = row_index<PAGED>(p, b, pos);
-                kr[r] = ld_nt(reinterpret_cast<const u4*>(kbase + ri * rowb) + lchunk);
-                vr[r] = ld_nt(reinterpret_cast<const u4*>(vbase + ri * rowb) + lchunk);
-                if (Q8) {
-                    const size_t si = (ri * p.kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
-                    ksc[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
-                    vsc[r] = (float)*reinterpret_cast<const _Float16*>(p.v_scale + si);
-                }
-            } else {
-                kr[r] = u4{0, 0, 0, 0};
-                vr[r] = u4{0, 0, 0, 0};
-                if (Q8) { ksc[r] = 0.f; vsc[r] = 0.f; }
+            const size_t ri = row_index<PAGED>(p, b, max(min(pos, end - 1), start));
+            st.k[r] = ld_nt(reinterpret_cast<const u4*>(kbase + ri * rowb) + lchunk);
+            st.v[r] = ld_nt(reinterpret_cast<const u4*>(vbase + ri * rowb) + lchunk);
+            if (Q8) {
+                const size_t si = (ri * p.kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
+                st.ks[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
+                st.vs[r] = (float)*reinterpret_cast<const _Float16*>(p.v_scale + si);
             }
         }
     };
 
-    int t = wave;
-    if (t < ntiles) load_tile(t);
-    for (; t < ntiles; t += kWaves) {
-        // registers -> wave-private LDS tile
+    auto consume = [&](Stage& st, int t, int t_next) {
+        const int tbase = start + t * kTile;
+        // registers -> wave-private LDS tile (rows past the end as zeros)
 #pragma unroll
         for (int r = 0; r < Gm::NLD; ++r) {
             const int row = r * Gm::RPI + lrow;
+            const bool live = tbase + row < end;
             if (Q8) {
                 u4 lo, hi;
-                dequant16(kr[r], ksc[r], lo, hi);
+                dequant16(st.k[r], live ? st.ks[r] : 0.0f, lo, hi);
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32) = lo;
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32 + 16) = hi;
-                dequant16(vr[r], vsc[r], lo, hi);
+                dequant16(st.v[r], live ? st.vs[r] : 0.0f, lo, hi);
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32) = lo;
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32 + 16) = hi;
             } else {
-                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = kr[r];
-                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = vr[r];
+                const u4 z = u4{0, 0, 0, 0};
+                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = live ? st.k[r] : z;
+                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = live ? st.v[r] : z;
             }
         }
         // LDS operations of one wave complete in order: the reads below see these writes.
         __builtin_amdgcn_wave_barrier();
-        if (t + kWaves < ntiles) load_tile(t + kWaves);  // next tile in flight during the math
+        // Refill this stage while computing. Unconditional (a tile past the end re-reads
+        // the split's last row, an L2 hit) so no branch hides loads from the wait counter.
+        load_tile(st, t_next);
+        if (t >= ntiles) return;  // uniform: this stage held no tile
 
-        // S^T = K Q^T over two 16-row m-tiles
-        f4 sacc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+        // S^T[16 positions x 16 heads] = K Q^T
+        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-            for (int s = 0; s < Gm::KSTEPS; ++s) {
-                const h8 a = *reinterpret_cast<const h8*>(kl + (mt * 16 + col) * Gm::LROW + (s * 32 + kb * 8) * 2);
-                sacc[mt] = mfma16x16x32(a, qf[s], sacc[mt]);
-            }
+        for (int s = 0; s < Gm::KSTEPS; ++s) {
+            const h8 a = *reinterpret_cast<const h8*>(kl + col * Gm::LROW + (s * 32 + kb * 8) * 2);
+            sacc = mfma16x16x32(a, qf[s], sacc);
         }
 
-        // online softmax (log2 domain); lane column = query head, rows = positions
-        const int tbase = start + t * kTile;
-        float sc[8];
+        // online softmax (log2 domain); lane column = query head, rows kb*4 + i = positions
+        float sc[4];
         float mx = kNegBig;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int mt = j >> 2, i = j & 3;
-            float x = sacc[mt][i] * p.scale2;
+        for (int i = 0; i < 4; ++i) {
+            float x = sacc[i] * p.scale2;
             if (__builtin_isnan(x)) x = kNegBig;
-            const bool valid = tbase + mt * 16 + kb * 4 + i < end;
-            sc[j] = valid ? x : -__builtin_inff();
-            mx = fmaxf(mx, sc[j]);
+            sc[i] = tbase + kb * 4 + i < end ? x : -__builtin_inff();
+            mx = fmaxf(mx, sc[i]);
         }
         mx = wave_max_xor(mx, 16);
         mx = wave_max_xor(mx, 32);
         const float m_new = fmaxf(m_run, mx);
         const float da = m_run - m_new;
         const float alpha = da < kCut2 ? 0.0f : exp2_fast(da);
-        h8 pf;
+        h4 pf;
         float psum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float df = sc[j] - m_new;  // -inf for masked rows
-            const float e = df < kCut2 ? 0.0f : exp2_fast(df);
-            const _Float16 eh = (_Float16)e;
-            pf[j] = eh;
+        for (int i = 0; i < 4; ++i) {
+            const float df = sc[i] - m_new;  // -inf for masked rows
+            const _Float16 eh = (_Float16)(df < kCut2 ? 0.0f : exp2_fast(df));
+            pf[i] = eh;
             psum += (float)eh;
         }
         l_run = l_run * alpha + psum;
         m_run = m_new;
 
-        // O^T += V^T P^T; k index j of lane block kb <-> tile row (j<4 ? kb*4+j : 16+kb*4+j-4)
+        // O^T += V^T P^T over the 16 positions (k = kb*4 + i); V^T by one transposing LDS read
 #pragma unroll
         for (int dt = 0; dt < Gm::DTILES; ++dt) {
-            h8 va;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int row = (j < 4) ? (kb * 4 + j) : (16 + kb * 4 + (j - 4));
-                va[j] = *reinterpret_cast<const _Float16*>(vl + row * Gm::LROW + (dt * 16 + col) * 2);
-            }
-            o[dt] = mfma16x16x32(va, pf, o[dt] * alpha);
+            const h4 va = lds_read_tr16(vl + (kb * 4 + (col >> 2)) * Gm::LROW + (dt * 16 + 4 * (col & 3)) * 2);
+            o[dt] = mfma16x16x16(va, pf, o[dt] * alpha);
         }
         __builtin_amdgcn_wave_barrier();
+    };
+
+    // uniform trip count: groups of NST tiles of this wave (tiles wave, wave + kWaves, ...)
+    const int my_tiles = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+    const int groups = (my_tiles + NST - 1) / NST;
+    if (groups > 0) {
+#pragma unroll
+        for (int s = 0; s < NST; ++s) load_tile(st[s], wave + s * kWaves);
+    }
+    for (int gi = 0; gi < groups; ++gi) {
+#pragma unroll
+        for (int s = 0; s < NST; ++s) {
+            const int ts = wave + (gi * NST + s) * kWaves;
+            consume(st[s], ts, ts + NST * kWaves);
+        }
     }
 
     // ---- combine the four waves of the workgroup through LDS ----
@@ -257,85 +433,86 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
             reinterpret_cast<_Float16*>(p.out)[row * D + d] = out_half(r);
         } else {
             const size_t slot = row * p.nsplit_grid + split;
-            p.part_o[slot * D + d] = O;
+            st_agent(p.part_o + slot * D + d, O);
             if (d == 0) {
-                p.part_ml[slot * 2] = M;
-                p.part_ml[slot * 2 + 1] = L;
+                st_agent(p.part_ml + slot * 2, M);
+                st_agent(p.part_ml + slot * 2 + 1, L);
             }
+        }
+    }
+
+    // rotated q back into the q buffer once no other workgroup of the group reads it
+    auto write_q = [&]() {
+        if (ROPE && gvalid) {
+            uint16_t* qrow = const_cast<uint16_t*>(p.q) + ((size_t)b * p.Hq + head) * D;
+#pragma unroll
+            for (int s = 0; s < Gm::KSTEPS; ++s) *reinterpret_cast<h8*>(qrow + s * 32 + kb * 8) = qf[s];
+        }
+    };
+    if (nsp == 1) write_q();
+
+    // Fused merge: the last workgroup of this (sequence, kv head, head block) to
+    // arrive merges the partials of its query heads and re-arms the counter.
+    if (nsp > 1 && p.counters) {
+        __shared__ int s_last;
+        // The partials were written through to the device coherence point (sc1 stores);
+        // wait until every one of them has completed before this workgroup is counted.
+        wait_vmem();
+        __syncthreads();
+        if (tid == 0) {
+            int* cnt = p.counters + (size_t)b * gridDim.y + blockIdx.y;
+            const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = prev == nsp - 1;
+            if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (s_last) {
+            merge_heads<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, reinterpret_cast<float*>(smem));
+            write_q();
         }
     }
 }
 
-// Log-sum-exp merge of the split partials of one query head (one workgroup per
-// (sequence, head)): M = max m_s, w_s = exp(m_s - M) (0 below -50),
-// out = sum w_s o_s / sum w_s l_s  (attention_kernels.cu:207-235).
+// Second pass of the two-kernel path: one workgroup per (sequence, head).
 template <int D, bool PAGED>
 __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
-    constexpr int NP = kThreads / D;  // split partitions summed per output element
-    __shared__ float s_w[kNsplitCap];
-    __shared__ float s_red[kWaves];
-    __shared__ float s_acc[NP][D];
-    const int row = blockIdx.x;       // b * Hq + head
-    const int b = row / p.Hq;
-    const int S = context_len(p, b, PAGED);
-    const int nsp = split_count(S);
+    __shared__ __align__(16) float lds[merge_lds_bytes<D>() / 4];
+    const int row = blockIdx.x;  // b * Hq + head
+    const int S = context_len(p, row / p.Hq, PAGED);
+    const int nsp = split_count(S, p.min_chunk, p.max_splits);
     if (p.single || nsp <= 1) return;  // the decode kernel wrote the output
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float* ml = p.part_ml + (size_t)row * p.nsplit_grid * 2;
-    const float* po = p.part_o + (size_t)row * p.nsplit_grid * D;
-
-    float m = kNegBig;
-    for (int s = tid; s < nsp; s += kThreads) m = fmaxf(m, ml[2 * s]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = wave_max_xor(m, off);
-    if (lane == 0) s_red[wave] = m;
-    __syncthreads();
-    float M = s_red[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_red[w]);
-    __syncthreads();
-    float l = 0.0f;
-    for (int s = tid; s < nsp; s += kThreads) {
-        const float df = ml[2 * s] - M;
-        const float w = df < kCut2 ? 0.0f : exp2_fast(df);
-        s_w[s] = w;
-        l += w * ml[2 * s + 1];
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) l = wave_sum_xor(l, off);
-    if (lane == 0) s_red[wave] = l;
-    __syncthreads();
-    float L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) L += s_red[w];
-
-    const int d = tid % D, part = tid / D;
-    float acc = 0.0f;
-    for (int s = part; s < nsp; s += NP) acc += s_w[s] * po[(size_t)s * D + d];
-    s_acc[part][d] = acc;
-    __syncthreads();
-    if (part == 0) {
-        float a = 0.0f;
-#pragma unroll
-        for (int q = 0; q < NP; ++q) a += s_acc[q][d];
-        const float r = L > 1e-12f ? a / L : 0.0f;
-        reinterpret_cast<_Float16*>(p.out)[(size_t)row * D + d] = out_half(r);
-    }
+    merge_heads<D>(p, (size_t)row, 1, nsp, lds);
 }
 
 template <int D, bool PAGED, bool Q8>
 int launch_t(const DecodeParams& p, int batch, hipStream_t stream) {
     const dim3 grid(p.single ? 1 : p.nsplit_grid, p.Hkv * p.ngb, batch);
-    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8>), grid, dim3(kThreads), 0, stream, p);
+    if (p.rope_table) {
+        if (Q8 || !p.counters) return -2;  // the step needs the fused merge and fp16 caches
+        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, false, kStages, true>), grid, dim3(kThreads), 0, stream, p);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, kStages, false>), grid, dim3(kThreads), 0, stream, p);
     if (hipGetLastError() != hipSuccess) return -1;
-    if (!p.single) {
+    if (!p.single && !p.counters) {
         hipLaunchKernelGGL((fa_merge_kernel<D, PAGED>), dim3(batch * p.Hq), dim3(kThreads), 0, stream, p);
         if (hipGetLastError() != hipSuccess) return -1;
     }
     return 0;
 }
 
+__global__ void fa_zero_kernel(uint32_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
 }  // namespace
+
+int launch_zero_fill(void* ptr, size_t bytes, hipStream_t stream) {
+    const size_t n = bytes / 4;
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(fa_zero_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, stream, static_cast<uint32_t*>(ptr), n);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_decode(const DecodeParams& p, int head_dim, int batch, bool paged, bool q8, hipStream_t stream) {
     if (head_dim == 128) {

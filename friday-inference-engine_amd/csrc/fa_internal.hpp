@@ -10,23 +10,34 @@ namespace fa {
 
 // ---- split-K partition, a function of the context length only ----
 // Each workgroup (4 waves x 32-position tiles) covers `chunk` positions, a
-// multiple of 128. Up to kNsplitCap splits per (sequence, kv head). Because the
-// partition depends on S alone, a paged sequence and a contiguous cache with
-// the same rows reduce in the same order (bit-identical outputs).
+// multiple of 128: about S / min_chunk splits, at most max_splits per (sequence,
+// kv head head block). Because the partition depends on S (and the two library
+// constants) alone, a paged sequence and a contiguous cache with the same rows
+// reduce in the same order, so their outputs are bit-identical.
 constexpr int kSpan = 128;
 constexpr int kPageTokens = 16;  // paged_kv_cache.h:16 KV_BLOCK_SIZE
-constexpr int kNsplitCap = 128;
+constexpr int kMaxSplitsLimit = 128;
 
-__host__ __device__ inline int split_chunk(int S) {
-    const int t = (S + kSpan - 1) / kSpan;
-    const int ns = t < kNsplitCap ? t : kNsplitCap;
-    return ns > 0 ? kSpan * ((t + ns - 1) / ns) : kSpan;
+__host__ __device__ inline int split_bound(int S, int min_chunk, int max_splits) {
+    int ns = S > 0 ? (S + min_chunk - 1) / min_chunk : 1;
+    return ns < max_splits ? ns : max_splits;
 }
-__host__ __device__ inline int split_count(int S) {
+__host__ __device__ inline int split_chunk(int S, int min_chunk, int max_splits) {
+    const int ns = split_bound(S, min_chunk, max_splits);
+    const int c = S > 0 ? (S + ns - 1) / ns : 1;
+    return ((c + kSpan - 1) / kSpan) * kSpan;
+}
+__host__ __device__ inline int split_count(int S, int min_chunk, int max_splits) {
     if (S <= 0) return 1;
-    const int c = split_chunk(S);
+    const int c = split_chunk(S, min_chunk, max_splits);
     return (S + c - 1) / c;
 }
+
+// Library-wide partition constants (environment FRIDAY_ATTN_MIN_CHUNK /
+// FRIDAY_ATTN_MAX_SPLITS, read once); see fa_api.cpp.
+int min_chunk();
+int max_splits();
+int splits_for(int Hkv, int ngb);
 
 struct DecodeParams {
     const uint16_t* q;         // [B][Hq*D]
@@ -42,12 +53,22 @@ struct DecodeParams {
     int max_seq;               // S is clamped to this (grid was sized for it)
     float* part_o;             // [B*Hq][nsplit_grid][D]
     float* part_ml;            // [B*Hq][nsplit_grid][2]  (max in log2 units, sum)
+    int* counters;             // fused merge: [B][Hkv*ngb] arrival counters (zero between launches); null: merge kernel
     uint16_t* out;             // [B][Hq*D]
     int Hq, Hkv, G, ngb, nsplit_grid, kv_dim;
     int single;                // 1: one split covers the whole context, no merge
+    int min_chunk, max_splits; // split partition constants
     float scale2;              // softmax scale * log2(e)
+    // fused RoPE + KV append (decode step): the kernel rotates q itself, the
+    // workgroup owning position S-1 rotates k and writes the new K/V row, and the
+    // rotated q is written back to `q`. Null rope_table: plain decode.
+    const float* rope_table;   // [max_ctx][D/2][2]
+    const uint16_t* k_new;     // [B][kv_dim] raw k of the new token
+    const uint16_t* v_new;     // [B][kv_dim] v of the new token
+    int neox;
 };
 
+int launch_zero_fill(void* ptr, size_t bytes, hipStream_t stream);
 int launch_decode(const DecodeParams& p, int head_dim, int batch, bool paged, bool q8, hipStream_t stream);
 
 struct RopeParams {

@@ -19,7 +19,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libfriday_attn.so")
+LIB_PATH = os.environ.get("FRIDAY_ATTN_LIB") or os.path.join(HERE, "lib", "libfriday_attn.so")
 
 FA_OK = 0
 FA_ERR_INVALID = -1
@@ -43,10 +43,15 @@ API = [
     ("friday_attn_decode_fits_shared_memory", _I, [_I]),
     ("friday_attn_split_workspace_bytes", _SZ, [_I, _I]),
     ("friday_attn_decode_attention_split", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
+    ("friday_attn_decode_workspace_init", _I, [_P, _SZ, _P]),
+    ("friday_attn_decode_attention_fused", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
+    ("friday_attn_decode_step", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_prefill_supported", _I, [_I, _I, _I]),
     ("friday_attn_prefill_attention", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P]),
     ("friday_attn_paged_workspace_bytes", _SZ, [_I, _I, _I]),
     ("friday_attn_paged_rope_store_kv", _I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
+    ("friday_attn_paged_decode_step", _I,
+     [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_paged_decode_attention", _I,
      [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
 ]
@@ -118,6 +123,12 @@ class Hip:
             h.hipGetErrorString.restype = C.c_char_p
             h.hipGetErrorString.argtypes = [_I]
             h.hipDeviceGetAttribute.argtypes = [C.POINTER(C.c_int), _I, _I]
+            h.hipStreamBeginCapture.argtypes = [_P, _I]
+            h.hipStreamEndCapture.argtypes = [_P, C.POINTER(C.c_void_p)]
+            h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), _P, _P, _P, _SZ]
+            h.hipGraphLaunch.argtypes = [_P, _P]
+            h.hipGraphExecDestroy.argtypes = [_P]
+            h.hipGraphDestroy.argtypes = [_P]
             cls._h = h
         return cls._h
 
@@ -135,6 +146,39 @@ class Hip:
     @classmethod
     def sync(cls):
         cls.check(cls.lib().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class Stream:
+    """A default-priority HIP stream."""
+
+    def __init__(self):
+        s = C.c_void_p()
+        Hip.check(Hip.lib().hipStreamCreate(C.byref(s)), "hipStreamCreate")
+        self.s = s.value
+
+    def synchronize(self):
+        Hip.check(Hip.lib().hipStreamSynchronize(self.s), "hipStreamSynchronize")
+
+
+class Graph:
+    """Capture of the launches issued on `stream` by fn(), replayed with launch()."""
+
+    def __init__(self, stream: Stream, fn):
+        h = Hip.lib()
+        Hip.check(h.hipStreamBeginCapture(stream.s, 2), "hipStreamBeginCapture")  # relaxed mode
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            Hip.check(h.hipStreamEndCapture(stream.s, C.byref(g)), "hipStreamEndCapture")
+        self.graph = g.value
+        e = C.c_void_p()
+        Hip.check(h.hipGraphInstantiate(C.byref(e), self.graph, None, None, 0), "hipGraphInstantiate")
+        self.exec = e.value
+        self.stream = stream
+
+    def launch(self):
+        Hip.check(Hip.lib().hipGraphLaunch(self.exec, self.stream.s), "hipGraphLaunch")
 
 
 class DeviceBuffer:
@@ -260,6 +304,33 @@ def launchDecodeAttentionSplit(q, k_cache, v_cache, out, seq_len, d_pos, max_seq
                                                      _ptr(v_scale)))
 
 
+def decodeWorkspaceInit(workspace, workspace_bytes=None, stream=None):
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes
+    _check(load().friday_attn_decode_workspace_init(_ptr(workspace), workspace_bytes, stream))
+
+
+def launchDecodeAttentionFused(q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads, num_kv_heads,
+                               head_dim, workspace, stream=None, k_scale=None, v_scale=None, workspace_bytes=None):
+    """Split-K decode with the merge done by the last workgroup (one kernel)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_decode_attention_fused(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), seq_len,
+                                                     _ptr(d_pos), max_seq_len, num_heads, num_kv_heads, head_dim,
+                                                     _ptr(workspace), workspace_bytes, stream, _ptr(k_scale),
+                                                     _ptr(v_scale)))
+
+
+def decodeStep(q, k, v, k_layer, v_layer, out, d_pos, pos, max_ctx, num_heads, num_kv_heads, head_dim, rope_table,
+               neox, workspace, stream=None, workspace_bytes=None):
+    """RoPE + KV append + split-K decode attention + merge in one launch (fused workspace)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_decode_step(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(v_layer), _ptr(out),
+                                          _ptr(d_pos), pos, max_ctx, num_heads, num_kv_heads, head_dim,
+                                          _ptr(rope_table), int(neox), _ptr(workspace), workspace_bytes, stream))
+
+
 def prefillAttentionSupported(num_heads, num_kv_heads, head_dim) -> bool:
     return bool(load().friday_attn_prefill_supported(num_heads, num_kv_heads, head_dim))
 
@@ -281,6 +352,16 @@ def pagedRopeStoreKv(q, k, v, k_pool, v_pool, block_table, block_table_stride, s
                                                   _ptr(block_table), block_table_stride, _ptr(seq_lens), batch,
                                                   head_dim, num_q_heads, num_kv_heads, max_ctx, _ptr(rope_table),
                                                   int(neox), stream))
+
+
+def pagedDecodeStep(q, k, v, k_pool, v_pool, out, block_table, block_table_stride, seq_lens, batch, max_seq_len,
+                    num_heads, num_kv_heads, head_dim, rope_table, neox, workspace, stream=None, workspace_bytes=None):
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_paged_decode_step(_ptr(q), _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool), _ptr(out),
+                                                _ptr(block_table), block_table_stride, _ptr(seq_lens), batch,
+                                                max_seq_len, num_heads, num_kv_heads, head_dim, _ptr(rope_table),
+                                                int(neox), _ptr(workspace), workspace_bytes, stream))
 
 
 def launchPagedDecodeAttention(q, k_pool, v_pool, out, block_table, block_table_stride, seq_lens, batch,

@@ -103,6 +103,34 @@ int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, c
                                        int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
                                        void* stream, const uint16_t* k_scale, const uint16_t* v_scale);
 
+/* Zeroes a decode workspace (a small fill kernel, no hipMemset node). Required once,
+ * after allocation, before the workspace is used by friday_attn_decode_attention_fused
+ * or friday_attn_paged_decode_attention; those calls leave it ready for the next call. */
+int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+/* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
+ * workgroup of each kv head to finish (an arrival counter in the workspace) instead of
+ * by a second kernel. Same arguments, same results bit for bit as
+ * friday_attn_decode_attention_split; the workspace must have been initialised with
+ * friday_attn_decode_workspace_init. Calls that share a workspace must not overlap. */
+int friday_attn_decode_attention_fused(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out,
+                                       int seq_len, const int* d_pos, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                                       void* stream, const uint16_t* k_scale, const uint16_t* v_scale);
+
+/* One decode layer-step in a single launch: friday_attn_rope_store_kv (T = 1) followed
+ * by friday_attn_decode_attention_fused over S = P + 1 positions, P = *d_pos (or pos),
+ * i.e. the sequence transformer.cpp:1044-1052 issues as two launches (ropeStoreKvKernel,
+ * then launchDecodeAttentionSplit). Every workgroup rotates q itself; the one whose
+ * split holds position P writes rotated k and raw v into row P of k_layer / v_layer;
+ * the rotated q is written back to q. Unlike ropeStoreKvKernel, k is not rotated in
+ * place (the rotated row lives in the cache). Outputs are bit-identical to the
+ * two-call sequence. Workspace as for friday_attn_decode_attention_fused
+ * (friday_attn_split_workspace_bytes(num_heads, max_ctx), initialised once). */
+int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
+                            uint16_t* out, const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,
+                            int head_dim, const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* ---------------- prefill attention ----------------
  * friday_attn::prefillAttentionSupported / launchPrefillAttention
  * (attention_kernels.h:46-50, .cu:649-684): causal attention of T queries at
@@ -120,7 +148,8 @@ int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const 
  * (experimental/runtime/src/kernels/paged_attention.cu:18-45, paged_kv_cache.h:16).
  * seq_lens[b] = context length of sequence b AFTER its append (device int32).
  * Every sequence gives the same result, bit for bit, as the contiguous-cache
- * friday_attn_decode_attention_split over the same logical rows. */
+ * friday_attn_decode_attention_split over the same logical rows. The decode uses the
+ * fused merge: its workspace must be initialised once with friday_attn_decode_workspace_init. */
 size_t friday_attn_paged_workspace_bytes(int batch, int num_heads, int max_seq_len);
 /* Append one token per sequence at position seq_lens[b] - 1 (RoPE as above).
  * q [B][Hq*d], k/v [B][Hkv*d] rotated in place. */
@@ -128,6 +157,14 @@ int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v,
                                     const int32_t* block_table, int block_table_stride, const int32_t* seq_lens,
                                     int batch, int head_dim, int num_q_heads, int num_kv_heads, int max_ctx,
                                     const float* rope_table, int neox, void* stream);
+/* Append (position seq_lens[b] - 1) plus decode attention for all sequences in one
+ * launch: friday_attn_paged_rope_store_kv followed by friday_attn_paged_decode_attention,
+ * with the same single-launch rules as friday_attn_decode_step (k not rotated in place). */
+int friday_attn_paged_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_pool,
+                                  uint16_t* v_pool, uint16_t* out, const int32_t* block_table,
+                                  int block_table_stride, const int32_t* seq_lens, int batch, int max_seq_len,
+                                  int num_heads, int num_kv_heads, int head_dim, const float* rope_table, int neox,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 int friday_attn_paged_decode_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                                        uint16_t* out, const int32_t* block_table, int block_table_stride,
                                        const int32_t* seq_lens, int batch, int max_seq_len, int num_heads,

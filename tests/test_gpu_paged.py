@@ -64,6 +64,7 @@ def test_paged_matches_contiguous(gpu, oracle, nseq, lo, hi, Hq, Hkv, d):
     dl = fa.DeviceBuffer.from_array(np.array(lens, np.int32))
     out = fa.DeviceBuffer(q.nbytes)
     ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(nseq, Hq, max_seq))
+    fa.decodeWorkspaceInit(ws)
     fa.launchPagedDecodeAttention(dq, dk, dv, out, dt, table.shape[1], dl, nseq, max_seq, Hq, Hkv, d, ws)
     fa.Hip.sync()
     got = out.download((nseq, Hq * d), np.uint16)
@@ -93,6 +94,7 @@ def test_paged_append_then_decode(gpu, oracle):
                         bufs["l"], nseq, d, Hq, Hkv, max_seq, bufs["r"], 1)
     out = fa.DeviceBuffer(q.nbytes)
     ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(nseq, Hq, max_seq))
+    fa.decodeWorkspaceInit(ws)
     fa.launchPagedDecodeAttention(bufs["q"], bufs["kp"], bufs["vp"], out, bufs["t"], table.shape[1], bufs["l"],
                                   nseq, max_seq, Hq, Hkv, d, ws)
     fa.Hip.sync()

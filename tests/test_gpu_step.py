@@ -1,0 +1,133 @@
+"""GPU parity of the one-launch decode layer-step (RoPE + KV append + split-K decode + merge).
+
+Bar: cache rows and rotated q bit-exact vs the oracle append; attention output
+bit-identical to the two-launch sequence (rope_store_kv, then the fused split
+decode) and within tolerance of the oracle; paged step bit-identical to the
+contiguous step per sequence.
+"""
+import numpy as np
+import pytest
+
+from fa_helpers import as_f32, assert_close, f16
+
+pytestmark = pytest.mark.gpu
+
+
+def run_step_vs_two_launch(fa, oracle, Hq, Hkv, d, S, max_ctx, base, neox, devpos, seed):
+    rng = np.random.default_rng(seed)
+    kv_dim = Hkv * d
+    kc = f16(rng, (max_ctx, kv_dim))
+    vc = f16(rng, (max_ctx, kv_dim))
+    q, k, v = f16(rng, (1, Hq * d), 2.0), f16(rng, (1, kv_dim)), f16(rng, (1, kv_dim))
+    pos = S - 1
+    table = fa.rope_table_host(max_ctx, d, base)
+    dt = fa.DeviceBuffer.from_array(table)
+    dpos = fa.DeviceBuffer.from_array(np.array([pos], np.int32))
+    ws_bytes = fa.splitAttentionWorkspaceBytes(Hq, max_ctx)
+
+    # one launch
+    b1 = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q, k=k, v=v, kc=kc, vc=vc).items()}
+    out1 = fa.DeviceBuffer(q.nbytes)
+    ws1 = fa.DeviceBuffer(ws_bytes)
+    fa.decodeWorkspaceInit(ws1)
+    fa.decodeStep(b1["q"], b1["k"], b1["v"], b1["kc"], b1["vc"], out1, dpos if devpos else None,
+                  0 if devpos else pos, max_ctx, Hq, Hkv, d, dt, neox, ws1)
+    # two launches
+    b2 = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q, k=k, v=v, kc=kc, vc=vc).items()}
+    out2 = fa.DeviceBuffer(q.nbytes)
+    ws2 = fa.DeviceBuffer(ws_bytes)
+    fa.decodeWorkspaceInit(ws2)
+    fa.ropeStoreKv(b2["q"], b2["k"], b2["v"], b2["kc"], b2["vc"], dpos if devpos else None, 0 if devpos else pos, 1,
+                   d, Hq, Hkv, max_ctx, dt, neox)
+    fa.launchDecodeAttentionFused(b2["q"], b2["kc"], b2["vc"], out2, 0 if devpos else S, dpos if devpos else None,
+                                  max_ctx, Hq, Hkv, d, ws2)
+    fa.Hip.sync()
+
+    qr, kr = q.copy(), k.copy()
+    oracle.rope_append(qr, kr, v, kc, vc, table, pos, Hq, Hkv, d, neox)
+    assert np.array_equal(b1["kc"].download(kc.shape, np.uint16), kc), "k cache after step"
+    assert np.array_equal(b1["vc"].download(vc.shape, np.uint16), vc), "v cache after step"
+    assert np.array_equal(b1["q"].download(q.shape, np.uint16), qr), "rotated q written back"
+    assert np.array_equal(b1["k"].download(k.shape, np.uint16), k), "k input left unrotated"
+    g1 = out1.download(Hq * d, np.uint16)
+    g2 = out2.download(Hq * d, np.uint16)
+    assert np.array_equal(g1, g2), "step differs from the two-launch sequence"
+    assert_close(as_f32(g1), oracle.decode(qr[0], kc, vc, S, Hq, Hkv, d), f"step S={S}")
+    return ws1
+
+
+@pytest.mark.parametrize("Hq,Hkv,d,S,max_ctx,base,neox,devpos", [
+    (14, 2, 64, 513, 1024, 1e6, 1, True),       # config 1: append at 512, attend 513
+    (32, 8, 128, 4096, 4096, 5e5, 0, True),     # config 2 shapes, interleaved pairs
+    (40, 8, 128, 32768, 32768, 1e6, 1, True),   # config 3 headline
+    (40, 8, 128, 1, 64, 1e6, 1, False),         # first token
+    (40, 8, 128, 300, 512, 1e6, 1, False),
+    (64, 4, 128, 2000, 2048, 1e6, 1, True),     # G = 16
+    (48, 1, 128, 999, 1024, 1e4, 0, True),      # G = 48: three head blocks
+])
+def test_step_matches_two_launches(gpu, oracle, Hq, Hkv, d, S, max_ctx, base, neox, devpos):
+    run_step_vs_two_launch(gpu, oracle, Hq, Hkv, d, S, max_ctx, base, neox, devpos, seed=S + Hq)
+
+
+def test_step_workspace_rearms(gpu, oracle):
+    """Counters return to zero: consecutive steps on one workspace keep the bits."""
+    fa = gpu
+    Hq, Hkv, d, max_ctx = 40, 8, 128, 4096
+    rng = np.random.default_rng(21)
+    kv_dim = Hkv * d
+    kc, vc = f16(rng, (max_ctx, kv_dim)), f16(rng, (max_ctx, kv_dim))
+    table = fa.DeviceBuffer.from_array(fa.rope_table_host(max_ctx, d, 1e6))
+    ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_ctx))
+    fa.decodeWorkspaceInit(ws)
+    dkc, dvc = fa.DeviceBuffer.from_array(kc), fa.DeviceBuffer.from_array(vc)
+    out = fa.DeviceBuffer(Hq * d * 2)
+    for pos in (1000, 1001, 1002, 3000):
+        q, k, v = f16(rng, (1, Hq * d)), f16(rng, (1, kv_dim)), f16(rng, (1, kv_dim))
+        dq, dk, dv = (fa.DeviceBuffer.from_array(a) for a in (q, k, v))
+        dpos = fa.DeviceBuffer.from_array(np.array([pos], np.int32))
+        fa.decodeStep(dq, dk, dv, dkc, dvc, out, dpos, 0, max_ctx, Hq, Hkv, d, table, 1, ws)
+        fa.Hip.sync()
+        qr = q.copy()
+        oracle.rope_append(qr, k.copy(), v, kc, vc, table.download((max_ctx, d // 2, 2), np.float32), pos, Hq, Hkv,
+                           d, 1)
+        assert_close(as_f32(out.download(Hq * d, np.uint16)), oracle.decode(qr[0], kc, vc, pos + 1, Hq, Hkv, d),
+                     f"pos {pos}")
+
+
+def test_paged_step_matches_contiguous_step(gpu):
+    """BASELINE config 5 in one launch: every sequence equals the contiguous step bit for bit."""
+    from test_gpu_paged import build_paged
+    fa = gpu
+    Hq, Hkv, d, nseq, PAGE = 40, 8, 128, 9, 16
+    kv_dim = Hkv * d
+    rng = np.random.default_rng(55)
+    lens = [int(x) for x in rng.integers(256, 5000, nseq)]  # after the append
+    max_seq = 5120
+    seqs, table, k_pool, v_pool = build_paged(rng, lens, kv_dim, max_seq)
+    q, k, v = f16(rng, (nseq, Hq * d)), f16(rng, (nseq, kv_dim)), f16(rng, (nseq, kv_dim))
+    rope = fa.DeviceBuffer.from_array(fa.rope_table_host(max_seq, d, 1e6))
+    bufs = {n: fa.DeviceBuffer.from_array(a) for n, a in
+            dict(q=q, k=k, v=v, kp=k_pool, vp=v_pool, t=table, l=np.array(lens, np.int32)).items()}
+    out = fa.DeviceBuffer(q.nbytes)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(nseq, Hq, max_seq))
+    fa.decodeWorkspaceInit(ws)
+    fa.pagedDecodeStep(bufs["q"], bufs["k"], bufs["v"], bufs["kp"], bufs["vp"], out, bufs["t"], table.shape[1],
+                       bufs["l"], nseq, max_seq, Hq, Hkv, d, rope, 1, ws)
+    fa.Hip.sync()
+    got = out.download((nseq, Hq * d), np.uint16)
+    got_kp = bufs["kp"].download(k_pool.shape, np.uint16)
+    for b, S in enumerate(lens):
+        kc = np.zeros((max_seq, kv_dim), np.uint16)
+        vc = np.zeros_like(kc)
+        kc[:S], vc[:S] = seqs[b]
+        dq, dk, dv = (fa.DeviceBuffer.from_array(a) for a in (q[b:b + 1], k[b:b + 1], v[b:b + 1]))
+        dkc, dvc = fa.DeviceBuffer.from_array(kc), fa.DeviceBuffer.from_array(vc)
+        o1 = fa.DeviceBuffer(Hq * d * 2)
+        w1 = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_seq))
+        fa.decodeWorkspaceInit(w1)
+        dpos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
+        fa.decodeStep(dq, dk, dv, dkc, dvc, o1, dpos, 0, max_seq, Hq, Hkv, d, rope, 1, w1)
+        fa.Hip.sync()
+        assert np.array_equal(got[b], o1.download(Hq * d, np.uint16)), f"seq {b} S={S}"
+        row = dkc.download((max_seq, kv_dim), np.uint16)[S - 1]
+        assert np.array_equal(got_kp[table[b, (S - 1) // PAGE], (S - 1) % PAGE], row), f"k row seq {b}"
