@@ -92,7 +92,6 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
     constexpr int K = kMaxSplitsLimit;
     float* s_m = lds;            // [HB][K]  max of each split, then its weight
     float* s_l = s_m + HB * K;   // [HB][K]  sum of each split, then weight * sum
-    float* s_L = s_l + HB * K;   // [HB]
     const int tid = threadIdx.x;
     const int hh = tid / C4, c = tid % C4;
     const int npad = (nsp + 7) & ~7;  // padded entries: max -inf, sum 0 -> weight exactly 0
@@ -103,22 +102,34 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
         const bool act = hh < hn;
         const size_t orow = row0 + h0 + (act ? hh : 0);
         const uint32_t obase = (uint32_t)(((h0 + (act ? hh : 0)) * p.nsplit_grid * D + 4 * c) * 4);
-        // first batch of this thread's partial columns, issued before the weights are known
+        // (max, sum) of every split first: the weights need them before anything else
+        constexpr int NR = (HB * K + kThreads - 1) / kThreads;
+        float2 mlv[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = tid + r * kThreads;
+            const int h = i / npad, sp = i - h * npad;
+            mlv[r] = i < hn * npad ? ld_coherent2(rml, (uint32_t)(((h0 + h) * p.nsplit_grid + min(sp, nsp - 1)) * 8))
+                                   : float2{0.f, 0.f};
+        }
+        // then this thread's partial columns, in flight while the weights are computed
         f4 ov[kMergeBatch];
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
-        for (int i = tid; i < hn * npad; i += kThreads) {
-            const int h = i / npad, sp = i - h * npad;
-            const float2 ml = ld_coherent2(rml, (uint32_t)(((h0 + h) * p.nsplit_grid + min(sp, nsp - 1)) * 8));
-            const float m = ml.x, l = ml.y;
-            s_m[h * K + sp] = sp < nsp ? m : -__builtin_inff();
-            s_l[h * K + sp] = sp < nsp ? l : 0.0f;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = tid + r * kThreads;
+            if (i < hn * npad) {
+                const int h = i / npad, sp = i - h * npad;
+                s_m[h * K + sp] = sp < nsp ? mlv[r].x : -__builtin_inff();
+                s_l[h * K + sp] = sp < nsp ? mlv[r].y : 0.0f;
+            }
         }
         __syncthreads();
         // one thread per (head, split): the head's max, then this split's weight
-        float wgt[(HB * K + kThreads - 1) / kThreads], wl[(HB * K + kThreads - 1) / kThreads];
+        float wgt[NR], wl[NR];
 #pragma unroll
-        for (int r = 0; r < (HB * K + kThreads - 1) / kThreads; ++r) {
+        for (int r = 0; r < NR; ++r) {
             const int i = tid + r * kThreads;
             wgt[r] = 0.0f;
             wl[r] = 0.0f;
@@ -136,7 +147,7 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
         }
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < (HB * K + kThreads - 1) / kThreads; ++r) {
+        for (int r = 0; r < NR; ++r) {
             const int i = tid + r * kThreads;
             if (i < hn * npad) {
                 const int h = i / npad, sp = i - h * npad;
@@ -145,25 +156,23 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
             }
         }
         __syncthreads();
-        if (tid < hn) {  // L in a fixed order: eight interleaved partial sums, then a tree
-            const float* wlh = s_l + tid * K;
+        if (act) {
+            // L in a fixed order (eight interleaved partial sums, then a tree), the same in
+            // every thread of the head
+            const float* wlh = s_l + hh * K;
             float Lp[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) Lp[k] = 0.0f;
             for (int t = 0; t < npad; t += 8)
 #pragma unroll
                 for (int k = 0; k < 8; ++k) Lp[k] += wlh[t + k];
-            s_L[tid] = ((Lp[0] + Lp[1]) + (Lp[2] + Lp[3])) + ((Lp[4] + Lp[5]) + (Lp[6] + Lp[7]));
-        }
-        __syncthreads();
-        if (act) {
+            const float L = ((Lp[0] + Lp[1]) + (Lp[2] + Lp[3])) + ((Lp[4] + Lp[5]) + (Lp[6] + Lp[7]));
             const float* w = s_m + hh * K;
             f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < kMergeBatch; ++j)
                 if (j < nsp) acc += w[j] * ov[j];
             for (int sp = kMergeBatch; sp < nsp; ++sp) acc += w[sp] * ld_coherent4(ro, obase + (uint32_t)(sp * D * 4));
-            const float L = s_L[hh];
             h4 o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
@@ -181,8 +190,12 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     using Gm = Geo<D, Q8>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
 
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y / p.ngb, gb = blockIdx.y % p.ngb;
+    // grid x = (kv head, head block) group, y = split: consecutive workgroup ids walk the
+    // groups first, so the dispatch order interleaves groups and, with round-robin
+    // placement over the 8 XCDs, the splits of one group share an XCD when there are 8 groups
+    const int group = blockIdx.x;
+    const int split = blockIdx.y;
+    const int kvh = group / p.ngb, gb = group % p.ngb;
     const int b = blockIdx.z;
     const int S = context_len(p, b, PAGED);
     const int chunk = p.single ? (S > 0 ? ((S + kSpan - 1) / kSpan) * kSpan : kSpan)
@@ -460,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         wait_vmem();
         __syncthreads();
         if (tid == 0) {
-            int* cnt = p.counters + (size_t)b * gridDim.y + blockIdx.y;
+            int* cnt = p.counters + (size_t)b * gridDim.x + group;
             const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last = prev == nsp - 1;
             if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -486,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
 
 template <int D, bool PAGED, bool Q8>
 int launch_t(const DecodeParams& p, int batch, hipStream_t stream) {
-    const dim3 grid(p.single ? 1 : p.nsplit_grid, p.Hkv * p.ngb, batch);
+    const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
     if (p.rope_table) {
         if (Q8 || !p.counters) return -2;  // the step needs the fused merge and fp16 caches
         hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, false, kStages, true>), grid, dim3(kThreads), 0, stream, p);

@@ -1,0 +1,105 @@
+// Header-only C++17 drop-in for the reference's friday_attn:: launchers
+// (attention_kernels.h:7-52) and for the direct ropeStoreKvKernel / storeKvQ8Kernel
+// launches of transformer.cpp, implemented on the friday_attn C ABI.
+//
+// Same names, argument order and meaning; tensors are taken as void pointers so
+// that half* / __half* / uint16_t* arguments all convert. Errors throw
+// std::runtime_error with the library's message, as the reference launchers do
+// (attention_kernels.cu:416-427, 431-441, 450-454, 483-485); an unsupported
+// prefill layout prints and aborts like launchPrefillAttention (:657-661).
+#ifndef FRIDAY_ATTN_HPP
+#define FRIDAY_ATTN_HPP
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <stdexcept>
+#include <string>
+
+#include "friday_attn.h"
+
+namespace friday_attn {
+
+namespace detail {
+inline void check(int rc) {
+    if (rc != FA_OK) throw std::runtime_error(std::string("friday_attn: ") + friday_attn_last_error());
+}
+inline const uint16_t* h(const void* p) { return static_cast<const uint16_t*>(p); }
+inline uint16_t* h(void* p) { return static_cast<uint16_t*>(p); }
+}  // namespace detail
+
+// ---- attention_kernels.h:18-20
+inline void launchDecodeAttention(const void* q, const void* k_cache, const void* v_cache, void* out, int seq_len,
+                                  int num_heads, int num_kv_heads, int head_dim, hipStream_t stream) {
+    detail::check(friday_attn_decode_attention(detail::h(q), detail::h(k_cache), detail::h(v_cache), detail::h(out),
+                                               seq_len, num_heads, num_kv_heads, head_dim, stream));
+}
+
+// ---- attention_kernels.h:24-26
+inline void launchDecodeAttentionDevPos(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                        const int* d_pos, int max_seq_len, int num_heads, int num_kv_heads,
+                                        int head_dim, hipStream_t stream) {
+    detail::check(friday_attn_decode_attention_dev_pos(detail::h(q), detail::h(k_cache), detail::h(v_cache),
+                                                       detail::h(out), d_pos, max_seq_len, num_heads, num_kv_heads,
+                                                       head_dim, stream));
+}
+inline bool decodeAttentionFitsSharedMemory(int max_seq_len) {
+    return friday_attn_decode_fits_shared_memory(max_seq_len) != 0;
+}
+
+// ---- attention_kernels.h:32-38 (the workspace holds splitAttentionWorkspaceBytes bytes, as there)
+inline size_t splitAttentionWorkspaceBytes(int num_heads, int max_seq_len) {
+    return friday_attn_split_workspace_bytes(num_heads, max_seq_len);
+}
+inline void launchDecodeAttentionSplit(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                       int seq_len, const int* d_pos, int max_seq_len, int num_heads,
+                                       int num_kv_heads, int head_dim, void* workspace, hipStream_t stream,
+                                       const void* k_scale = nullptr, const void* v_scale = nullptr) {
+    detail::check(friday_attn_decode_attention_split(
+        detail::h(q), k_cache, v_cache, detail::h(out), seq_len, d_pos, max_seq_len, num_heads, num_kv_heads,
+        head_dim, workspace, splitAttentionWorkspaceBytes(num_heads, max_seq_len), stream, detail::h(k_scale),
+        detail::h(v_scale)));
+}
+
+// ---- attention_kernels.h:46-50
+inline bool prefillAttentionSupported(int num_heads, int num_kv_heads, int head_dim) {
+    return friday_attn_prefill_supported(num_heads, num_kv_heads, head_dim) != 0;
+}
+inline void launchPrefillAttention(const void* q, const void* k_cache, const void* v_cache, void* out, int T,
+                                   const int* d_pos0, int num_heads, int num_kv_heads, int head_dim,
+                                   hipStream_t stream, const void* k_scale = nullptr,
+                                   const void* v_scale = nullptr) {
+    if (T <= 0) return;
+    if (!prefillAttentionSupported(num_heads, num_kv_heads, head_dim)) {
+        std::fprintf(stderr, "launchPrefillAttention: unsupported head layout\n");
+        std::abort();
+    }
+    detail::check(friday_attn_prefill_attention(detail::h(q), k_cache, v_cache, detail::h(out), T, d_pos0,
+                                                num_heads, num_kv_heads, head_dim, stream, detail::h(k_scale),
+                                                detail::h(v_scale)));
+}
+
+// ---- the kernels transformer.cpp launches directly
+// ropeStoreKvKernel (cuda_math_kernels.cu:363-404; T tokens = grid.y there); the rope
+// table replaces the (freq_base, freq_factors) kernel arguments: build it once with
+// friday_attn_rope_table_upload. k_layer == v_layer == nullptr: ropeKernel semantics.
+inline void ropeStoreKv(void* q, void* k, const void* v, void* k_layer, void* v_layer, const int* d_pos, int T,
+                        int head_dim, int num_q_heads, int num_kv_heads, int max_ctx, const float* rope_table,
+                        bool neox, hipStream_t stream) {
+    detail::check(friday_attn_rope_store_kv(detail::h(q), detail::h(k), detail::h(v), detail::h(k_layer),
+                                            detail::h(v_layer), d_pos, 0, T, head_dim, num_q_heads, num_kv_heads,
+                                            max_ctx, rope_table, neox ? 1 : 0, stream));
+}
+// storeKvQ8Kernel (cuda_math_kernels.cu:409-432)
+inline void storeKvQ8(const void* k, const void* v, int8_t* k_layer, void* k_scale, int8_t* v_layer, void* v_scale,
+                      const int* d_pos, int T, int kv_dim, int max_ctx, hipStream_t stream) {
+    detail::check(friday_attn_store_kv_q8(detail::h(k), detail::h(v), k_layer, detail::h(k_scale), v_layer,
+                                          detail::h(v_scale), d_pos, 0, T, kv_dim, max_ctx, stream));
+}
+
+}  // namespace friday_attn
+
+#endif  // FRIDAY_ATTN_HPP
