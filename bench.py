@@ -1,19 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the KV-cache path on one MI355X (BASELINE.json metric and configs).
 
-A step is one decode token through all layers of the headline workload
-(Qwen2.5-32B attention shapes, 40 query / 8 kv heads,
-head_dim 128, fp16 KV, context 32768 after the append, 64 layers' caches
-resident in HBM): per layer, RoPE + KV append at position S-1 followed by
-split-K decode attention with the log-sum-exp merge. The 64-layer step is
-captured once into a HIP graph (as the reference captures its decode layers
-into a CUDA graph, transformer.cpp:1465-1483) and replayed.
+Default (the driver's line): BASELINE config 3, the headline. A step is one
+decode token through all 64 layers at Qwen2.5-32B attention shapes (40 query /
+8 kv heads, head_dim 128, fp16 KV, context 32768 after the append, all 64
+layers' caches resident in HBM, 8 GiB): per layer ONE launch of
+friday_attn_decode_step = RoPE + KV append at position S-1 + split-K GQA decode
+attention + log-sum-exp merge. The 64 launches are captured once into a HIP
+graph (the reference captures its decode layers into a CUDA graph,
+transformer.cpp:1465-1483) and replayed; layers run back to back, each one
+after the previous one finished, as in a real decode step.
 
-Prints ONE JSON line. `value` is the K/V bytes the attention must read per
-layer-step (2*S*Hkv*d*2) divided by the measured time per layer-step (append +
-attention), in GB/s. The same line carries the per-layer-step time, the decode
-kernel's roofline record (HIP events around every decode launch inside the
-timed graph replays) and the reference CPU attention timed on this host.
+`value` = K/V bytes the attention must read per layer-step (2*S*Hkv*d*2 =
+134,217,728 B) / measured time per layer-step, in GB/s. `roofline` is that of
+the one kernel a layer-step launches (fa_decode_kernel, step variant): its
+average duration = timed-region time / launches, from HIP events on the
+stream the graph runs on. `cpu_baseline` times the reference's own CPU
+attention (cpu_ops.cpp decodeAttention compiled from source into oracle/_ref)
+on this host.
+
+--config all additionally prints one JSON line per other BASELINE config
+(1: Qwen2.5-0.5B shapes; 2: 32 layers at 1k/4k/8k, cold and warm; 3 at 16k;
+4: chunked prefill on MFMA with MFMA utilisation; 5: 16 paged sequences).
 """
 from __future__ import annotations
 
@@ -28,11 +36,127 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "friday-inference-engine_amd"))
 
 METRIC = "decode-attn µs/layer-step + KV GB/s (% HBM peak) at 32k ctx, 40q/8kv d128"
-HBM_PEAK_GBS = 8000.0
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+MALL_BYTES = 256 << 20         # Infinity Cache: a "cold" working set must exceed it
+
+# HBM traffic of one step-kernel launch at the headline shape, from rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by the copy-kernel calibration
+# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): 135.16 MB fetched + 0.76 MB written per launch.
+HEADLINE_TRAFFIC_BYTES = 135919326
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+class Ctx:
+    """HIP plumbing shared by the measurements."""
+
+    def __init__(self):
+        import friday_attn as fa
+
+        self.fa = fa
+        fa.load()
+        if fa.Hip.device_count() < 1:
+            raise SystemExit("no HIP device")
+        self.bk = C.CDLL(os.path.join(ROOT, "friday-inference-engine_amd", "lib", "libfa_benchkit.so"))
+        self.bk.fabk_fill_normal_f16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
+        self.stream = fa.Stream()
+
+    def fill(self, buf, n_half, seed, scale=1.0):
+        self.bk.fabk_fill_normal_f16(buf.ptr, n_half, seed, scale, self.stream.s)
+
+    def timed(self, fn, steps, warmup):
+        """Capture fn's launches into a graph; replay warmup + steps times; ms per replay."""
+        fa = self.fa
+        graph = fa.Graph(self.stream, fn)
+        for _ in range(warmup):
+            graph.launch()
+        self.stream.synchronize()
+        t0, t1 = fa.Event(), fa.Event()
+        t0.record(self.stream.s)
+        for _ in range(steps):
+            graph.launch()
+        t1.record(self.stream.s)
+        self.stream.synchronize()
+        return t0.elapsed_ms(t1) / steps
+
+
+class DecodeLayers:
+    """`sets` x `L` layer caches [S][Hkv*d] fp16 plus per-layer q/k/v/out and one workspace."""
+
+    def __init__(self, cx, S, L, Hq, Hkv, d, sets=1, seed=0):
+        import numpy as np
+
+        fa = cx.fa
+        self.cx, self.S, self.L, self.Hq, self.Hkv, self.d, self.sets = cx, S, L, Hq, Hkv, d, sets
+        self.kv_dim = Hkv * d
+        self.layer_bytes = S * self.kv_dim * 2
+        n = sets * L
+        self.k = fa.DeviceBuffer(n * self.layer_bytes)
+        self.v = fa.DeviceBuffer(n * self.layer_bytes)
+        cx.fill(self.k, n * S * self.kv_dim, 1 + seed)
+        cx.fill(self.v, n * S * self.kv_dim, 2 + seed)
+        rng = np.random.default_rng(seed)
+        f16 = lambda shape: rng.standard_normal(shape, dtype=np.float32).astype(np.float16).view(np.uint16)
+        self.q = fa.DeviceBuffer.from_array(f16((n, Hq * d)))
+        self.kn = fa.DeviceBuffer.from_array(f16((n, self.kv_dim)))
+        self.vn = fa.DeviceBuffer.from_array(f16((n, self.kv_dim)))
+        self.out = fa.DeviceBuffer(n * Hq * d * 2)
+        self.table = fa.DeviceBuffer(fa.rope_table_bytes(S, d))
+        fa.rope_table_upload(self.table, S, d, 1e6)
+        self.pos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
+        self.ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, S))
+        fa.decodeWorkspaceInit(self.ws, stream=cx.stream.s)
+        cx.stream.synchronize()
+
+    def ptrs(self, i):
+        return (self.q.ptr + i * self.Hq * self.d * 2, self.kn.ptr + i * self.kv_dim * 2,
+                self.vn.ptr + i * self.kv_dim * 2, self.k.ptr + i * self.layer_bytes,
+                self.v.ptr + i * self.layer_bytes, self.out.ptr + i * self.Hq * self.d * 2)
+
+    def step(self, s):
+        """One decode step of layer set s: one launch per layer."""
+        fa, cx = self.cx.fa, self.cx
+        for l in range(self.L):
+            q, kn, vn, kc, vc, out = self.ptrs(s * self.L + l)
+            fa.decodeStep(q, kn, vn, kc, vc, out, self.pos, 0, self.S, self.Hq, self.Hkv, self.d, self.table, 1,
+                          self.ws, cx.stream.s)
+
+    def decode_only(self, s):
+        fa, cx = self.cx.fa, self.cx
+        for l in range(self.L):
+            q, _, _, kc, vc, out = self.ptrs(s * self.L + l)
+            fa.launchDecodeAttentionFused(q, kc, vc, out, 0, self.pos, self.S, self.Hq, self.Hkv, self.d, self.ws,
+                                          cx.stream.s)
+
+    def measure(self, steps, warmup, fn="step"):
+        """ms per decode step; with several sets each replay walks all of them (cold caches)."""
+        f = getattr(self, fn)
+        ms = self.cx.timed(lambda: [f(s) for s in range(self.sets)], steps, warmup)
+        return ms / self.sets
+
+    def check_layer0(self):
+        import numpy as np
+
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        from py_oracle import Oracle
+
+        S, Hq, Hkv, d = self.S, self.Hq, self.Hkv, self.d
+        q0 = self.q.download(Hq * d, np.uint16)
+        k0 = self.k.download((S, self.kv_dim), np.uint16)
+        v0 = self.v.download((S, self.kv_dim), np.uint16)
+        got = self.out.download(Hq * d, np.uint16).view(np.float16).astype(np.float32)
+        ref = Oracle().decode(q0, k0, v0, S, Hq, Hkv, d)
+        err = np.abs(got - ref)
+        ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
+        log(f"[bench] layer 0 vs oracle: max_abs {err.max():.2e} {'PASS' if ok else 'FAIL'}")
+        return {"layer0_vs_oracle_max_abs": float(err.max()), "pass": ok}
+
+    def free(self):
+        for b in (self.k, self.v, self.q, self.kn, self.vn, self.out, self.table, self.pos, self.ws):
+            b.free()
 
 
 def cpu_baseline(S, Hq, Hkv, d, budget_s):
@@ -43,7 +167,7 @@ def cpu_baseline(S, Hq, Hkv, d, budget_s):
     import py_oracle
 
     ncpu = os.cpu_count() or 1
-    threads = max(1, min(16, ncpu, Hq))  # per-head parallelism; the box's CPU share is 16
+    threads = max(1, min(16, ncpu, Hq))  # parallel over query heads; the GPU box's CPU share is 16
     rng = np.random.default_rng(0)
     kv_dim = Hkv * d
     kc = rng.standard_normal((S, kv_dim), dtype=np.float32).astype(np.float16).astype(np.float32)
@@ -66,143 +190,35 @@ def cpu_baseline(S, Hq, Hkv, d, budget_s):
         run()
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
+        if el >= budget_s or n >= 1000:
             break
     us = el / n * 1e6
-    gbs = 2 * S * kv_dim * 4 / (us * 1e-6) / 1e9
     return {"value": round(us, 1), "unit": "us/layer-step", "cores": threads, "kind": kind,
-            "kv_gbs_fp32": round(gbs, 2),
-            "sample": f"{n} calls of one layer (ctx {S}, {Hq}q/{Hkv}kv d{d}, fp32 cache of fp16 values), "
+            "kv_gbs_fp32": round(2 * S * kv_dim * 4 / (us * 1e-6) / 1e9, 2),
+            "sample": f"{n} calls of one layer (ctx {S}, {Hq}q/{Hkv}kv d{d}, fp32 cache holding fp16 values), "
                       f"{el:.1f} s; {what}; host logical CPUs {ncpu}"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--ctx", type=int, default=32768)
-    ap.add_argument("--layers", type=int, default=64)
-    ap.add_argument("--heads", type=int, default=40)
-    ap.add_argument("--kv-heads", type=int, default=8)
-    ap.add_argument("--head-dim", type=int, default=128)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--merge", choices=("step", "fused", "kernel"), default="step",
-                    help="step: RoPE+append+decode+merge in one launch per layer; fused: append launch + "
-                         "decode with last-workgroup merge; kernel: append + decode + merge kernel")
-    args = ap.parse_args()
-
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the KV-cache path is built and "
-              f"measured on a single MI355X; multi-GPU sharding is a design note, not a run.", file=sys.stderr)
-        sys.exit(2)
-
-    import numpy as np
-
-    import friday_attn as fa
-
-    lib = fa.load()
-    bk = C.CDLL(os.path.join(ROOT, "friday-inference-engine_amd", "lib", "libfa_benchkit.so"))
-    bk.fabk_fill_normal_f16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
-    if fa.Hip.device_count() < 1:
-        raise SystemExit("no HIP device")
-
-    S, L, Hq, Hkv, d = args.ctx, args.layers, args.heads, args.kv_heads, args.head_dim
-    kv_dim = Hkv * d
-    layer_elems = S * kv_dim
-    log(f"[bench] config3 S={S} layers={L} {Hq}q/{Hkv}kv d{d}: allocating "
-        f"{2 * L * layer_elems * 2 / 2**30:.2f} GiB of KV cache")
-    stream = fa.Stream()
-    kcache = fa.DeviceBuffer(L * layer_elems * 2)
-    vcache = fa.DeviceBuffer(L * layer_elems * 2)
-    bk.fabk_fill_normal_f16(kcache.ptr, L * layer_elems, 1, 1.0, stream.s)
-    bk.fabk_fill_normal_f16(vcache.ptr, L * layer_elems, 2, 1.0, stream.s)
-    rng = np.random.default_rng(0)
-    f16 = lambda shape: rng.standard_normal(shape, dtype=np.float32).astype(np.float16).view(np.uint16)
-    qs = fa.DeviceBuffer.from_array(f16((L, Hq * d)))
-    ks = fa.DeviceBuffer.from_array(f16((L, kv_dim)))
-    vs = fa.DeviceBuffer.from_array(f16((L, kv_dim)))
-    outs = fa.DeviceBuffer(L * Hq * d * 2)
-    table = fa.DeviceBuffer(fa.rope_table_bytes(S, d))
-    fa.rope_table_upload(table, S, d, 1e6)
-    dpos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
-    ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, S))
-    fa.decodeWorkspaceInit(ws, stream=stream.s)
-    launch = fa.launchDecodeAttentionSplit if args.merge == "kernel" else fa.launchDecodeAttentionFused
-    stream.synchronize()
-
-    def step():
-        for l in range(L):
-            kl = kcache.ptr + l * layer_elems * 2
-            vl = vcache.ptr + l * layer_elems * 2
-            ql = qs.ptr + l * Hq * d * 2
-            if args.merge == "step":
-                fa.decodeStep(ql, ks.ptr + l * kv_dim * 2, vs.ptr + l * kv_dim * 2, kl, vl, outs.ptr + l * Hq * d * 2,
-                              dpos, 0, S, Hq, Hkv, d, table, 1, ws, stream.s)
-                continue
-            fa.ropeStoreKv(ql, ks.ptr + l * kv_dim * 2, vs.ptr + l * kv_dim * 2, kl, vl, dpos, 0, 1, d, Hq, Hkv,
-                           S, table, 1, stream.s)
-            decode(l)
-
-    def decode(l):
-        kl = kcache.ptr + l * layer_elems * 2
-        vl = vcache.ptr + l * layer_elems * 2
-        ql = qs.ptr + l * Hq * d * 2
-        launch(ql, kl, vl, outs.ptr + l * Hq * d * 2, 0, dpos, S, Hq, Hkv, d, ws, stream.s)
-
-    def timed(graph, steps, warmup):
-        for _ in range(warmup):
-            graph.launch()
-        stream.synchronize()
-        t_start, t_end = fa.Event(), fa.Event()
-        w0 = time.perf_counter()
-        t_start.record(stream.s)
-        for _ in range(steps):
-            graph.launch()
-        t_end.record(stream.s)
-        stream.synchronize()
-        return t_start.elapsed_ms(t_end) / steps, time.perf_counter() - w0
-
-    # timed region 1: the whole step (append + attention, all layers)
-    ms_step, wall = timed(fa.Graph(stream, step), args.steps, args.warmup)
-    # timed region 2: the dominant kernel alone (decode attention of all layers, back to back)
-    ms_dec, _ = timed(fa.Graph(stream, lambda: [decode(l) for l in range(L)]), args.steps, args.warmup)
-    dec_mean = ms_dec * 1e3 / L
-
+def headline(cx, args):
+    S, L, Hq, Hkv, d = args.ctx, args.layers, 40, 8, 128
+    log(f"[bench] config 3: S={S} layers={L} {Hq}q/{Hkv}kv d{d}, {2 * L * S * Hkv * d * 2 / 2**30:.2f} GiB KV")
+    dl = DecodeLayers(cx, S, L, Hq, Hkv, d)
+    ms_step = dl.measure(args.steps, args.warmup, "step")
+    ms_dec = dl.measure(args.steps, args.warmup, "decode_only")
+    check = None if args.no_check else dl.check_layer0()
+    dl.free()
     us_layer = ms_step * 1e3 / L
-    kv_bytes = 2 * S * kv_dim * 2
-    kv_gbs = kv_bytes / (us_layer * 1e-6) / 1e9
-    ach = kv_bytes / (dec_mean * 1e-6) / 1e9
-    log(f"[bench] merge={args.merge} min_chunk={os.environ.get('FRIDAY_ATTN_MIN_CHUNK', 'default')} "
-        f"max_splits={os.environ.get('FRIDAY_ATTN_MAX_SPLITS', 'default')}")
-    log(f"[bench] {ms_step:.3f} ms/step, {us_layer:.2f} us/layer-step, decode call {dec_mean:.2f} us, "
-        f"wall {wall:.2f} s")
-
-    check = None
-    if not args.no_check:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        from py_oracle import Oracle
-
-        q0 = qs.download(Hq * d, np.uint16)
-        k0 = kcache.download((S, kv_dim), np.uint16)
-        v0 = vcache.download((S, kv_dim), np.uint16)
-        got = outs.download(Hq * d, np.uint16).view(np.float16).astype(np.float32)
-        ref = Oracle().decode(q0, k0, v0, S, Hq, Hkv, d)
-        err = np.abs(got - ref)
-        ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
-        check = {"layer0_vs_oracle_max_abs": float(err.max()), "pass": ok}
-        log(f"[bench] layer 0 vs oracle: max_abs {err.max():.2e} {'PASS' if ok else 'FAIL'}")
-
+    kv_bytes = 2 * S * Hkv * d * 2
+    gbs = kv_bytes / (us_layer * 1e-6) / 1e9
+    log(f"[bench] {ms_step:.3f} ms/step, {us_layer:.2f} us/layer-step ({gbs:.0f} GB/s), "
+        f"decode-only launch {ms_dec * 1e3 / L:.2f} us")
     cpu = None
     if not args.no_cpu:
         log("[bench] timing the reference CPU attention ...")
         cpu = cpu_baseline(S, Hq, Hkv, d, args.cpu_seconds)
-
-    rec = {
+    return {
         "metric": METRIC,
-        "value": round(kv_gbs, 1),
+        "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -213,24 +229,141 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic: device-generated N(0,1) fp16 K/V caches, seeded N(0,1) q/k/v",
-        "config": {"workload": f"BASELINE config 3: decode step (RoPE+KV append, split-K GQA attention + LSE merge) "
-                               f"over {L} layers, ctx {S} after append, {Hq}q/{Hkv}kv d{d}, fp16 KV, batch 1, "
-                               f"HIP graph replay",
+        "config": {"workload": f"BASELINE config 3 (headline): decode step over {L} layers, one launch per layer "
+                               f"(RoPE + KV append + split-K GQA attention + LSE merge), ctx {S} after the append, "
+                               f"{Hq}q/{Hkv}kv d{d}, fp16 KV, batch 1, HIP graph replay",
                    "layers": L, "ctx": S, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": d},
         "us_per_layer_step": round(us_layer, 3),
-        "hbm_frac_step": round(kv_gbs / HBM_PEAK_GBS, 4),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(1e3 / ms_step, 2),
-        "decode_call_us": round(dec_mean, 3),
-        "roofline": {"bound": "hbm", "kernel": ("fa_decode_kernel + fa_merge_kernel (friday_attn_decode_attention_split)"
-                                if args.merge == "kernel" else
-                                "fa_decode_kernel (friday_attn_decode_attention_fused, last-workgroup merge)"),
-                     "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": kv_bytes},
+        "decode_only_launch_us": round(ms_dec * 1e3 / L, 3),
+        "roofline": {"bound": "hbm", "kernel": "fa_decode_kernel (step variant: friday_attn_decode_step)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": HEADLINE_TRAFFIC_BYTES,
+                     "algorithmic_bytes_per_launch": kv_bytes, "launches_per_step": L},
         "cpu_baseline": cpu,
         "check": check,
     }
-    print(json.dumps(rec), flush=True)
+
+
+def decode_config(cx, name, S, L, Hq, Hkv, d, steps, warmup, cold):
+    kv_bytes = 2 * S * Hkv * d * 2
+    sets = 1
+    if cold:  # rotate through enough layer sets that the working set exceeds the MALL 4x over
+        sets = max(1, -(-4 * MALL_BYTES // (kv_bytes * L)))
+    dl = DecodeLayers(cx, S, L, Hq, Hkv, d, sets=sets, seed=S)
+    ms = dl.measure(steps, warmup, "step")
+    dl.free()
+    us = ms * 1e3 / L
+    gbs = kv_bytes / (us * 1e-6) / 1e9
+    return {"config": name, "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}", "cache": "cold" if cold else "warm",
+            "working_set_MiB": round(sets * L * kv_bytes / 2**20, 1), "us_per_layer_step": round(us, 3),
+            "kv_GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(1e3 / ms, 1)}
+
+
+def prefill_config(cx, p0, steps, warmup):
+    """512-token causal chunk after p0 cached tokens, 40q/8kv d128, MFMA."""
+    import numpy as np
+
+    fa = cx.fa
+    T, Hq, Hkv, d = 512, 40, 8, 128
+    S = p0 + T
+    L = max(2, -(-2 * MALL_BYTES // (2 * S * Hkv * d * 2)))  # rotate caches beyond the MALL
+    lb = S * Hkv * d * 2
+    k, v = fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * lb)
+    cx.fill(k, L * S * Hkv * d, 5)
+    cx.fill(v, L * S * Hkv * d, 6)
+    q, out = fa.DeviceBuffer(T * Hq * d * 2), fa.DeviceBuffer(T * Hq * d * 2)
+    cx.fill(q, T * Hq * d, 7)
+    pos = fa.DeviceBuffer.from_array(np.array([p0], np.int32))
+    ms = cx.timed(lambda: [fa.launchPrefillAttention(q, k.ptr + l * lb, v.ptr + l * lb, out, T, pos, Hq, Hkv, d,
+                                                     cx.stream.s) for l in range(L)], steps, warmup) / L
+    for b in (k, v, q, out, pos):
+        b.free()
+    flops = 4.0 * d * Hq * (T * p0 + T * (T + 1) / 2)  # causal (unmasked) QK^T and PV flops
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"config": "4: chunked prefill", "T": T, "p0": p0, "heads": f"{Hq}q/{Hkv}kv d{d}",
+            "us_per_chunk": round(ms * 1e3, 2), "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
+            "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "tokens_per_s": round(T / (ms * 1e-3), 0)}
+
+
+def paged_config(cx, steps, warmup):
+    """16 sequences, S ~ U[256, 16k], 16-token pages in a permuted pool, one launch."""
+    import numpy as np
+
+    fa = cx.fa
+    B, Hq, Hkv, d, P = 16, 40, 8, 128, 16
+    kv_dim = Hkv * d
+    rng = np.random.default_rng(5)
+    lens = rng.integers(256, 16384 + 1, B).astype(np.int32)
+    max_seq = 16384
+    nblk = [(int(s) + P - 1) // P for s in lens]
+    perm = rng.permutation(sum(nblk)).astype(np.int32)
+    table = np.full((B, max_seq // P), -1, np.int32)
+    at = 0
+    for b in range(B):
+        table[b, :nblk[b]] = perm[at:at + nblk[b]]
+        at += nblk[b]
+    pool_rows = sum(nblk) * P
+    kp, vp = fa.DeviceBuffer(pool_rows * kv_dim * 2), fa.DeviceBuffer(pool_rows * kv_dim * 2)
+    cx.fill(kp, pool_rows * kv_dim, 8)
+    cx.fill(vp, pool_rows * kv_dim, 9)
+    bufs = [fa.DeviceBuffer.from_array(a) for a in (table, lens)]
+    q = fa.DeviceBuffer(B * Hq * d * 2)
+    kn, vn, out = fa.DeviceBuffer(B * kv_dim * 2), fa.DeviceBuffer(B * kv_dim * 2), fa.DeviceBuffer(B * Hq * d * 2)
+    for bb, n in ((q, B * Hq * d), (kn, B * kv_dim), (vn, B * kv_dim)):
+        cx.fill(bb, n, 10)
+    rope = fa.DeviceBuffer(fa.rope_table_bytes(max_seq, d))
+    fa.rope_table_upload(rope, max_seq, d, 1e6)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(B, Hq, max_seq))
+    fa.decodeWorkspaceInit(ws, stream=cx.stream.s)
+    ms = cx.timed(lambda: fa.pagedDecodeStep(q, kn, vn, kp, vp, out, bufs[0], table.shape[1], bufs[1], B, max_seq,
+                                             Hq, Hkv, d, rope, 1, ws, cx.stream.s), steps, warmup)
+    for bb in (kp, vp, q, kn, vn, out, rope, ws, *bufs):
+        bb.free()
+    kv_bytes = float(lens.sum()) * kv_dim * 2 * 2
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    return {"config": "5: paged multi-sequence step", "sequences": B, "sum_ctx": int(lens.sum()),
+            "pool_MiB": round(2 * pool_rows * kv_dim * 2 / 2**20, 1), "us_per_step": round(ms * 1e3, 2),
+            "kv_GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(B / (ms * 1e-3), 0)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--config", choices=("headline", "all", "others"), default="headline",
+                    help="headline: the driver's one line; all/others: also (only) the other BASELINE configs")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the KV-cache path is built and measured "
+              f"on a single MI355X; how it would shard is a design note, not a run.", file=sys.stderr)
+        sys.exit(2)
+
+    cx = Ctx()
+    if args.config in ("headline", "all"):
+        print(json.dumps(headline(cx, args)), flush=True)
+    if args.config in ("all", "others"):
+        lines = [decode_config(cx, "1: Qwen2.5-0.5B layer", 513, 24, 14, 2, 64, args.steps, args.warmup, False)]
+        for S in (1024, 4096, 8192):
+            for cold in (True, False):
+                lines.append(decode_config(cx, "2: 32q/8kv x 32 layers", S, 32, 32, 8, 128, args.steps, args.warmup,
+                                           cold))
+        lines.append(decode_config(cx, "3: 40q/8kv x 64 layers", 16384, 64, 40, 8, 128, args.steps, args.warmup,
+                                   False))
+        for p0 in (0, 1024, 2048, 4096, 7680):
+            lines.append(prefill_config(cx, p0, args.steps, args.warmup))
+        lines.append(paged_config(cx, args.steps, args.warmup))
+        for rec in lines:
+            print(json.dumps(rec), flush=True)
 
 
 if __name__ == "__main__":

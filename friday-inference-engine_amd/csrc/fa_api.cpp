@@ -96,7 +96,7 @@ namespace fa {
 // Split partition: about S / min_chunk splits of >= min_chunk positions, at most
 // max_splits (a multiple of 128 and <= 256 respectively).
 int min_chunk() {
-    static const int v = env_int("FRIDAY_ATTN_MIN_CHUNK", 256, 1, 1 << 20) / kSpan * kSpan;
+    static const int v = env_int("FRIDAY_ATTN_MIN_CHUNK", 128, 1, 1 << 20) / kSpan * kSpan;
     return v < kSpan ? kSpan : v;
 }
 int max_splits() {

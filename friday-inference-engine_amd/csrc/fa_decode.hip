@@ -20,6 +20,8 @@
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
+#include <type_traits>
+
 namespace fa {
 namespace {
 
@@ -30,6 +32,7 @@ constexpr int kTile = 16;  // positions per wave tile
 #define FA_DECODE_STAGES 1
 #endif
 constexpr int kStages = FA_DECODE_STAGES;  // register stages (tiles in flight) per wave
+constexpr int kShortStages = 4;            // stages when a wave has at most this many tiles
 
 template <int D, bool Q8>
 struct Geo {
@@ -84,8 +87,8 @@ __device__ __forceinline__ void dequant16(u4 raw, float sc, u4& lo, u4& hi) {
 // (nh = heads of the group) give the same bits. Partials are read with loads that
 // bypass the caches: in the fused path other workgroups of this launch wrote them
 // through to memory just before.
-constexpr int kMergeBatch = 32;  // partial rows loaded per round trip
-template <int D>
+// NB: partial rows per thread loaded in one round trip (8 or 32, >= nsp when possible)
+template <int D, int NB>
 __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
     constexpr int C4 = D / 4;
     constexpr int HB = kThreads / C4;  // heads per pass
@@ -113,9 +116,9 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
                                    : float2{0.f, 0.f};
         }
         // then this thread's partial columns, in flight while the weights are computed
-        f4 ov[kMergeBatch];
+        f4 ov[NB];
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
+        for (int j = 0; j < NB; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             const int i = tid + r * kThreads;
@@ -170,9 +173,9 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
             const float* w = s_m + hh * K;
             f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < kMergeBatch; ++j)
+            for (int j = 0; j < NB; ++j)
                 if (j < nsp) acc += w[j] * ov[j];
-            for (int sp = kMergeBatch; sp < nsp; ++sp) acc += w[sp] * ld_coherent4(ro, obase + (uint32_t)(sp * D * 4));
+            for (int sp = NB; sp < nsp; ++sp) acc += w[sp] * ld_coherent4(ro, obase + (uint32_t)(sp * D * 4));
             h4 o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
@@ -180,6 +183,14 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
         }
         __syncthreads();  // LDS reused by the next pass
     }
+}
+
+template <int D>
+__device__ __forceinline__ void merge_any(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
+    if (nsp <= 8)
+        merge_heads<D, 8>(p, row0, nh, nsp, lds);
+    else
+        merge_heads<D, 32>(p, row0, nh, nsp, lds);
 }
 
 template <int D>
@@ -302,7 +313,6 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         u4 k[Gm::NLD], v[Gm::NLD];
         float ks[Gm::NLD], vs[Gm::NLD];
     };
-    Stage st[NST];
 
     auto load_tile = [&](Stage& st, int t) {
         if (ROPE && t == append_tile && wave == append_wave) wait_vmem();  // the appended row is stored
@@ -393,20 +403,30 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         __builtin_amdgcn_wave_barrier();
     };
 
-    // uniform trip count: groups of NST tiles of this wave (tiles wave, wave + kWaves, ...)
+    // uniform trip count: groups of N tiles of this wave (tiles wave, wave + kWaves, ...).
+    // Long splits keep one tile in flight per wave (more congests HBM); short ones, whose
+    // waves have at most four tiles, issue them all at once (one memory latency).
     const int my_tiles = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
-    const int groups = (my_tiles + NST - 1) / NST;
-    if (groups > 0) {
+    auto stream = [&](auto n_tag) {
+        constexpr int N = decltype(n_tag)::value;
+        Stage st[N];
+        const int groups = (my_tiles + N - 1) / N;
+        if (groups > 0) {
 #pragma unroll
-        for (int s = 0; s < NST; ++s) load_tile(st[s], wave + s * kWaves);
-    }
-    for (int gi = 0; gi < groups; ++gi) {
-#pragma unroll
-        for (int s = 0; s < NST; ++s) {
-            const int ts = wave + (gi * NST + s) * kWaves;
-            consume(st[s], ts, ts + NST * kWaves);
+            for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * kWaves);
         }
-    }
+        for (int gi = 0; gi < groups; ++gi) {
+#pragma unroll
+            for (int s = 0; s < N; ++s) {
+                const int ts = wave + (gi * N + s) * kWaves;
+                consume(st[s], ts, ts + N * kWaves);
+            }
+        }
+    };
+    if ((ntiles + kWaves - 1) / kWaves <= kShortStages)
+        stream(std::integral_constant<int, kShortStages>{});
+    else
+        stream(std::integral_constant<int, NST>{});
 
     // ---- combine the four waves of the workgroup through LDS ----
     l_run = wave_sum_xor(l_run, 16);
@@ -480,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         }
         __syncthreads();
         if (s_last) {
-            merge_heads<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, reinterpret_cast<float*>(smem));
+            merge_any<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, reinterpret_cast<float*>(smem));
             write_q();
         }
     }
@@ -494,7 +514,7 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
     const int S = context_len(p, row / p.Hq, PAGED);
     const int nsp = split_count(S, p.min_chunk, p.max_splits);
     if (p.single || nsp <= 1) return;  // the decode kernel wrote the output
-    merge_heads<D>(p, (size_t)row, 1, nsp, lds);
+    merge_any<D>(p, (size_t)row, 1, nsp, lds);
 }
 
 template <int D, bool PAGED, bool Q8>
