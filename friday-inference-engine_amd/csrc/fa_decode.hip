@@ -223,74 +223,122 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     const int head = kvh * p.G + g;
 
     // Q^T as the B operand of S^T = K Q^T: lane (col = head, kb) holds q[d = s*32 + kb*8 .. +8].
+    // Loads are unconditional (lanes past the group read the group's first head and are
+    // zeroed later), so no branch drains the load counter.
     h8 qf[Gm::KSTEPS];
     {
-        const uint16_t* qrow = p.q + ((size_t)b * p.Hq + (gvalid ? head : 0)) * D;
+        const uint16_t* qrow = p.q + ((size_t)b * p.Hq + (gvalid ? head : kvh * p.G)) * D;
 #pragma unroll
         for (int s = 0; s < Gm::KSTEPS; ++s) {
-            u4 raw = gvalid ? *reinterpret_cast<const u4*>(qrow + s * 32 + kb * 8) : u4{0, 0, 0, 0};
-            qf[s] = *reinterpret_cast<h8*>(&raw);
+            const u4 raw = *reinterpret_cast<const u4*>(qrow + s * 32 + kb * 8);
+            qf[s] = *reinterpret_cast<const h8*>(&raw);
         }
     }
 
-    int append_wave = -1, append_tile = -1;
-    if (ROPE && S > 0) {
-        // rotate this lane's q fragment at the new token's position S-1; both halves of
-        // every rotation pair sit in the same lane (neox: k-steps s and s + KSTEPS/2,
-        // interleaved: neighbouring elements of one fragment)
-        constexpr int HD2 = D / 2;
-        const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)(S - 1) * HD2;
+    // Step variant: the RoPE table entries of this lane's q fragment, and the new K/V row
+    // chunk (plus its rotation partner chunk) of lane chunk `lane % CPR`, all at position
+    // S-1. They are issued before the first K/V tile and used after it is in flight.
+    constexpr int HD2 = D / 2;
+    constexpr int QCS = ROPE ? (Gm::KSTEPS / 2) * 8 : 1;  // table entries of the q fragment (neox)
+    float2 qcs[QCS];
+    u4 nk = u4{0, 0, 0, 0}, nkp = u4{0, 0, 0, 0}, nv = u4{0, 0, 0, 0};
+    float2 ncs[ROPE ? 8 : 1];
+    int append_wave = -1, append_tile = -1, append_row = -1;
+    const int nchunk = (lane % Gm::CPR) * 8;  // first element of this lane's fp16 row chunk
+    if constexpr (ROPE) {
+        const int pos = S > 0 ? S - 1 : 0;
+        const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
         if (p.neox) {
 #pragma unroll
             for (int s = 0; s < Gm::KSTEPS / 2; ++s)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float2 c = cs[s * 32 + kb * 8 + j];
-                    _Float16 r0, r1;
-                    rope_rotate((float)qf[s][j], (float)qf[s + Gm::KSTEPS / 2][j], c.x, c.y, r0, r1);
-                    qf[s][j] = r0;
-                    qf[s + Gm::KSTEPS / 2][j] = r1;
-                }
-        } else {
+                for (int j = 0; j < 8; ++j) qcs[s * 8 + j] = cs[s * 32 + kb * 8 + j];
+        }
+        const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
+        const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
+        nk = *reinterpret_cast<const u4*>(p.k_new + src + nchunk);
+        nkp = *reinterpret_cast<const u4*>(p.k_new + src + partner);
+        nv = *reinterpret_cast<const u4*>(p.v_new + src + nchunk);
 #pragma unroll
-            for (int s = 0; s < Gm::KSTEPS; ++s)
+        for (int j = 0; j < 8; ++j) ncs[j] = cs[p.neox ? (nchunk % HD2) + j : (nchunk + j) / 2];
+        // the wave that loads the tile holding position S-1 (in the split holding it)
+        // takes the new row from registers instead of the cache; past max_seq: no append
+        const int s_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
+        if (S > 0 && split == nsp - 1 && s_raw == S) {
+            const int last_tile = (end - start - 1) / kTile;
+            append_wave = last_tile % kWaves;
+            append_tile = last_tile;
+            append_row = (S - 1) - (start + last_tile * kTile);
+        }
+    }
+
+    // Rotate this lane's q fragment at position S-1 (neox pairs: k-steps s and
+    // s + KSTEPS/2; interleaved pairs: neighbouring elements), then zero lanes past the
+    // group. The new K row is rotated the same way and written to the cache by the
+    // append wave; that wave substitutes the rotated row in its own tile, so it never
+    // re-reads the cache row it wrote.
+    u4 rk = u4{0, 0, 0, 0};
+    auto prepare = [&]() __attribute__((always_inline)) {
+        if constexpr (ROPE) {
+            if (p.neox) {
 #pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    const float2 c = cs[(s * 32 + kb * 8 + j) / 2];
-                    _Float16 r0, r1;
-                    rope_rotate((float)qf[s][j], (float)qf[s][j + 1], c.x, c.y, r0, r1);
-                    qf[s][j] = r0;
-                    qf[s][j + 1] = r1;
+                for (int s = 0; s < Gm::KSTEPS / 2; ++s)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float2 c = qcs[s * 8 + j];
+                        _Float16 r0, r1;
+                        rope_rotate((float)qf[s][j], (float)qf[s + Gm::KSTEPS / 2][j], c.x, c.y, r0, r1);
+                        qf[s][j] = r0;
+                        qf[s + Gm::KSTEPS / 2][j] = r1;
+                    }
+            } else {
+                const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)(S > 0 ? S - 1 : 0) * HD2;
+#pragma unroll
+                for (int s = 0; s < Gm::KSTEPS; ++s)
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        const float2 c = cs[(s * 32 + kb * 8 + j) / 2];
+                        _Float16 r0, r1;
+                        rope_rotate((float)qf[s][j], (float)qf[s][j + 1], c.x, c.y, r0, r1);
+                        qf[s][j] = r0;
+                        qf[s][j + 1] = r1;
+                    }
+            }
+            if (wave == append_wave) {
+                const h8 x = *reinterpret_cast<const h8*>(&nk);
+                const h8 y = *reinterpret_cast<const h8*>(&nkp);
+                h8 r;
+                if (p.neox) {
+                    const bool lo = nchunk < HD2;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        _Float16 r0, r1;
+                        // pair (i, i + D/2): x0 is the low-half element
+                        rope_rotate((float)(lo ? x[j] : y[j]), (float)(lo ? y[j] : x[j]), ncs[j].x, ncs[j].y, r0, r1);
+                        r[j] = lo ? r0 : r1;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        _Float16 r0, r1;
+                        rope_rotate((float)x[j], (float)x[j + 1], ncs[j].x, ncs[j].y, r0, r1);
+                        r[j] = r0;
+                        r[j + 1] = r1;
+                    }
                 }
+                rk = *reinterpret_cast<const u4*>(&r);
+                if (lane < Gm::CPR) {
+                    const size_t dst = row_index<PAGED>(p, b, S - 1) * p.kv_dim + (size_t)kvh * D + nchunk;
+                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.k)) + dst) = rk;
+                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.v)) + dst) = nv;
+                }
+            }
         }
         if (!gvalid) {
 #pragma unroll
             for (int s = 0; s < Gm::KSTEPS; ++s) qf[s] = h8{0, 0, 0, 0, 0, 0, 0, 0};
         }
-        // the wave that will load the tile holding position S-1 (in the split holding it)
-        // writes the new row of this kv head; it waits for its own stores just before it
-        // issues that tile's loads (same wave, same L2: then the loads see the row)
-        const int s_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
-        const int last_tile = (end - start - 1) / kTile;
-        append_wave = (split == nsp - 1 && s_raw == S) ? last_tile % kWaves : -1;  // past max_seq: no append
-        append_tile = last_tile;
-        if (wave == append_wave && lane < HD2) {
-            const int o0 = p.neox ? lane : 2 * lane, o1 = p.neox ? lane + HD2 : 2 * lane + 1;
-            const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
-            const _Float16* kn = reinterpret_cast<const _Float16*>(p.k_new) + src;
-            const _Float16* vn = reinterpret_cast<const _Float16*>(p.v_new) + src;
-            const float2 c = cs[lane];
-            _Float16 r0, r1;
-            rope_rotate((float)kn[o0], (float)kn[o1], c.x, c.y, r0, r1);
-            const size_t dst = row_index<PAGED>(p, b, S - 1) * p.kv_dim + (size_t)kvh * D;
-            _Float16* kd = const_cast<_Float16*>(reinterpret_cast<const _Float16*>(p.k)) + dst;
-            _Float16* vd = const_cast<_Float16*>(reinterpret_cast<const _Float16*>(p.v)) + dst;
-            kd[o0] = r0;
-            kd[o1] = r1;
-            vd[o0] = vn[o0];
-            vd[o1] = vn[o1];
-        }
-    }
+    };
 
     unsigned char* kl = smem + wave * Gm::WAVE_LDS;
     unsigned char* vl = kl + kTile * Gm::LROW;
@@ -315,7 +363,6 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     };
 
     auto load_tile = [&](Stage& st, int t) {
-        if (ROPE && t == append_tile && wave == append_wave) wait_vmem();  // the appended row is stored
         const int base = start + t * kTile;
 #pragma unroll
         for (int r = 0; r < Gm::NLD; ++r) {
@@ -348,8 +395,13 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32 + 16) = hi;
             } else {
                 const u4 z = u4{0, 0, 0, 0};
-                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = live ? st.k[r] : z;
-                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = live ? st.v[r] : z;
+                u4 kx = live ? st.k[r] : z, vx = live ? st.v[r] : z;
+                if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
+                    kx = rk;  // the new row, as written to the cache by this wave
+                    vx = nv;
+                }
+                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = kx;
+                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = vx;
             }
         }
         // LDS operations of one wave complete in order: the reads below see these writes.
@@ -415,6 +467,7 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * kWaves);
         }
+        prepare();
         for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
             for (int s = 0; s < N; ++s) {
