@@ -73,10 +73,11 @@ int env_int(const char* name, int dflt, int lo, int hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// Workspace: counters [B*Hq] int at offset 0 (the fused merge uses
-// B*Hkv*ceil(G/16) <= B*Hq of them; they must stay at a fixed place whatever the
-// split count of a call), then part_o [B*Hq][ns][d] fp32 and part_ml [B*Hq][ns][2].
-size_t counters_bytes(int batch, int Hq) { return ((size_t)batch * Hq * sizeof(int) + 255) / 256 * 256; }
+// Workspace: arrival counters [B*Hq], one int per 256 bytes, at offset 0 (the fused
+// merge uses B*Hkv*ceil(G/16) <= B*Hq of them; they must stay at a fixed place
+// whatever the split count of a call), then part_o [B*Hq][ns][d] fp32 and
+// part_ml [B*Hq][ns][2].
+size_t counters_bytes(int batch, int Hq) { return (size_t)batch * Hq * fa::kCounterStride * sizeof(int); }
 
 size_t split_ws_bytes(int batch, int Hq, int max_seq, int d) {
     const size_t ns = (size_t)fa::split_bound(max_seq, fa::min_chunk(), fa::max_splits());
@@ -210,6 +211,8 @@ static int decode_common(const char* w, const uint16_t* q, const void* k, const 
         const int grid_len = d_pos ? max_seq : seq_len;
         p.nsplit_grid = fa::split_bound(grid_len, p.min_chunk, p.max_splits);
         const size_t need = split_ws_bytes(1, Hq, grid_len, d);
+        if (need >= (size_t(1) << 31))  // partials are addressed with 32-bit buffer offsets
+            return fail(FA_ERR_UNSUPPORTED, "%s: split workspace beyond 2 GiB (%zu bytes)", w, need);
         if (!ws || ws_bytes < need)
             return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, ws_bytes);
         set_workspace(p, ws, 1, d, fused);
@@ -285,6 +288,8 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
     const int grid_len = d_pos ? max_ctx : pos + 1;
     p.nsplit_grid = fa::split_bound(grid_len, p.min_chunk, p.max_splits);
     const size_t need = split_ws_bytes(1, num_heads, grid_len, head_dim);
+    if (need >= (size_t(1) << 31))  // partials are addressed with 32-bit buffer offsets
+        return fail(FA_ERR_UNSUPPORTED, "%s: split workspace beyond 2 GiB (%zu bytes)", w, need);
     if (!workspace || workspace_bytes < need)
         return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
     set_workspace(p, workspace, 1, head_dim, true);
@@ -336,6 +341,8 @@ static int paged_decode_common(const char* w, uint16_t* q, const uint16_t* k_new
     p.max_splits = fa::splits_for(num_kv_heads, p.ngb);
     p.nsplit_grid = fa::split_bound(max_seq_len, p.min_chunk, p.max_splits);
     const size_t need = split_ws_bytes(batch, num_heads, max_seq_len, head_dim);
+    if (need >= (size_t(1) << 31))  // partials are addressed with 32-bit buffer offsets
+        return fail(FA_ERR_UNSUPPORTED, "%s: split workspace beyond 2 GiB (%zu bytes)", w, need);
     if (!workspace || workspace_bytes < need)
         return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
     set_workspace(p, workspace, batch, head_dim, true);

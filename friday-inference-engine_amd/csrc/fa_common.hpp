@@ -103,6 +103,13 @@ __device__ __forceinline__ float2 ld_coherent2(__amdgpu_buffer_rsrc_t r, uint32_
     return *reinterpret_cast<const float2*>(&x);
 }
 
+__device__ __forceinline__ void st_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const i4v*>(&v), r, (int)byte_off, 0, kCpolSc1);
+}
+__device__ __forceinline__ void st_coherent2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const i2v*>(&v), r, (int)byte_off, 0, kCpolSc1);
+}
+
 // s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
 // The memory clobber keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -45,7 +45,8 @@ struct Geo {
     static constexpr int RPI = 64 / CPR;              // rows per wave load
     static constexpr int NLD = kTile / RPI;           // loads per tile per tensor
     static constexpr int WAVE_LDS = 2 * kTile * LROW;  // K and V tile of one wave
-    static constexpr int COMB_LDS = kWaves * 16 * (D + 2) * 4;
+    static constexpr int CROW = D + 4;                 // combine row stride in floats (bank spread)
+    static constexpr int COMB_LDS = (2 * kWaves * 16 + kWaves * 16 * CROW) * 4;
     static constexpr int MERGE_LDS = (2 * (kThreads / (D / 4)) * 128 + 64) * 4;
     static constexpr int LDS0 = (kWaves * WAVE_LDS > COMB_LDS ? kWaves * WAVE_LDS : COMB_LDS);
     static constexpr int LDS = LDS0 > MERGE_LDS ? LDS0 : MERGE_LDS;
@@ -110,10 +111,11 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
         float2 mlv[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            const int i = tid + r * kThreads;
+            // unconditional (clamped) loads: a branch here would drain the load counter
+            // before the partial-O loads below are issued
+            const int i = min(tid + r * kThreads, hn * npad - 1);
             const int h = i / npad, sp = i - h * npad;
-            mlv[r] = i < hn * npad ? ld_coherent2(rml, (uint32_t)(((h0 + h) * p.nsplit_grid + min(sp, nsp - 1)) * 8))
-                                   : float2{0.f, 0.f};
+            mlv[r] = ld_coherent2(rml, (uint32_t)(((h0 + h) * p.nsplit_grid + min(sp, nsp - 1)) * 8));
         }
         // then this thread's partial columns, in flight while the weights are computed
         f4 ov[NB];
@@ -185,10 +187,84 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
     }
 }
 
+// The same merge for nsp <= NB, with no per-split branch or dependent LDS chain:
+// the (max, sum) table of a head is padded to NB entries (max -inf, sum 0, so the
+// weight is exactly 0), and every output thread reads its head's table with vector
+// LDS loads and computes the head's max and weights itself. The arithmetic and its
+// order are those of merge_heads, so both give the same bits.
+template <int D, int NB>
+__device__ void merge_short(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
+    constexpr int C4 = D / 4;
+    constexpr int HB = kThreads / C4;  // heads per pass
+    constexpr int NE = HB * NB;        // table entries per pass
+    constexpr int NR = (NE + kThreads - 1) / kThreads;  // table entries per thread
+    float* s_m = lds;        // [HB][NB]
+    float* s_l = s_m + NE;   // [HB][NB]
+    const int tid = threadIdx.x;
+    const int hh = tid / C4, c = tid % C4;
+    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(p.part_o + row0 * p.nsplit_grid * D, (uint32_t)(nh * p.nsplit_grid * D * 4));
+    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml + row0 * p.nsplit_grid * 2, (uint32_t)(nh * p.nsplit_grid * 8));
+    for (int h0 = 0; h0 < nh; h0 += HB) {
+        const int hn = min(HB, nh - h0);
+        const bool act = hh < hn;
+        const uint32_t obase = (uint32_t)(((h0 + (act ? hh : 0)) * p.nsplit_grid * D + 4 * c) * 4);
+        // this thread's table entries, then its partial columns: one memory round trip
+        float2 mlv[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int ei = min(tid + r * kThreads, hn * NB - 1);
+            mlv[r] = ld_coherent2(rml, (uint32_t)(((h0 + ei / NB) * p.nsplit_grid + min(ei % NB, nsp - 1)) * 8));
+        }
+        f4 ov[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int e = tid + r * kThreads;
+            if (e < NE) {
+                const bool live = e < hn * NB && e % NB < nsp;
+                s_m[e] = live ? mlv[r].x : -__builtin_inff();
+                s_l[e] = live ? mlv[r].y : 0.0f;
+            }
+        }
+        __syncthreads();
+        if (act) {
+            float m[NB], l[NB];
+#pragma unroll
+            for (int j = 0; j < NB; j += 4) {
+                *reinterpret_cast<f4*>(m + j) = *reinterpret_cast<const f4*>(s_m + hh * NB + j);
+                *reinterpret_cast<f4*>(l + j) = *reinterpret_cast<const f4*>(s_l + hh * NB + j);
+            }
+            float M = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < NB; ++j) M = fmaxf(M, m[j]);
+            float Lp[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) Lp[k] = 0.0f;
+            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const float df = m[j] - M;
+                const float w = df < kCut2 ? 0.0f : exp2_fast(df);
+                Lp[j % 8] += w * l[j];
+                acc += w * ov[j];
+            }
+            const float L = ((Lp[0] + Lp[1]) + (Lp[2] + Lp[3])) + ((Lp[4] + Lp[5]) + (Lp[6] + Lp[7]));
+            h4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
+            reinterpret_cast<h4*>(p.out + (row0 + h0 + hh) * D)[c] = o;
+        }
+        if (h0 + HB < nh) __syncthreads();  // LDS reused by the next pass
+    }
+}
+
 template <int D>
 __device__ __forceinline__ void merge_any(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
     if (nsp <= 8)
-        merge_heads<D, 8>(p, row0, nh, nsp, lds);
+        merge_short<D, 8>(p, row0, nh, nsp, lds);
+    else if (nsp <= 32)
+        merge_short<D, 32>(p, row0, nh, nsp, lds);
     else
         merge_heads<D, 32>(p, row0, nh, nsp, lds);
 }
@@ -487,43 +563,46 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     __syncthreads();  // all waves done with their tiles; LDS is reused
     float* cm = reinterpret_cast<float*>(smem);           // [kWaves][16]
     float* cl = cm + kWaves * 16;                          // [kWaves][16]
-    float* co = cl + kWaves * 16;                          // [kWaves][16][D]
+    float* co = cl + kWaves * 16;                          // [kWaves][16][CROW]
     if (kb == 0) {
         cm[wave * 16 + col] = m_run;
         cl[wave * 16 + col] = l_run;
     }
 #pragma unroll
     for (int dt = 0; dt < Gm::DTILES; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) co[(wave * 16 + col) * D + dt * 16 + kb * 4 + i] = o[dt][i];
+        *reinterpret_cast<f4*>(co + (wave * 16 + col) * Gm::CROW + dt * 16 + kb * 4) = o[dt];
     __syncthreads();
 
+    // one thread per (head, 4 consecutive output columns)
     const int gcount = min(16, p.G - gb * 16);
-    for (int idx = tid; idx < gcount * D; idx += kThreads) {
-        const int gg = idx / D, d = idx % D;
+    const __amdgpu_buffer_rsrc_t rpo = coherent_rsrc(p.part_o, 0x7fffffff);
+    const __amdgpu_buffer_rsrc_t rpml = coherent_rsrc(p.part_ml, 0x7fffffff);
+    for (int idx = tid; idx < gcount * (D / 4); idx += kThreads) {
+        const int gg = idx / (D / 4), d4 = idx % (D / 4);
         float M = cm[gg];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) M = fmaxf(M, cm[w * 16 + gg]);
-        float L = 0.0f, O = 0.0f;
+        float L = 0.0f;
+        f4 O = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             const float df = cm[w * 16 + gg] - M;
             const float wt = df < kCut2 ? 0.0f : exp2_fast(df);
             L += wt * cl[w * 16 + gg];
-            O += wt * co[(w * 16 + gg) * D + d];
+            O += wt * *reinterpret_cast<const f4*>(co + (w * 16 + gg) * Gm::CROW + 4 * d4);
         }
         const int hh = kvh * p.G + gb * 16 + gg;
         const size_t row = (size_t)b * p.Hq + hh;
         if (nsp == 1) {
-            const float r = L > 1e-12f ? O / L : 0.0f;
-            reinterpret_cast<_Float16*>(p.out)[row * D + d] = out_half(r);
+            h4 r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
+            *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(p.out) + row * D + 4 * d4) = r;
         } else {
+            // written through to the device coherence point (sc1) for the merging workgroup
             const size_t slot = row * p.nsplit_grid + split;
-            st_agent(p.part_o + slot * D + d, O);
-            if (d == 0) {
-                st_agent(p.part_ml + slot * 2, M);
-                st_agent(p.part_ml + slot * 2 + 1, L);
-            }
+            st_coherent4(rpo, (uint32_t)((slot * D + 4 * d4) * 4), O);
+            if (d4 == 0) st_coherent2(rpml, (uint32_t)(slot * 8), float2{M, L});
         }
     }
 
@@ -546,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         wait_vmem();
         __syncthreads();
         if (tid == 0) {
-            int* cnt = p.counters + (size_t)b * gridDim.x + group;
+            int* cnt = p.counters + ((size_t)b * gridDim.x + group) * kCounterStride;
             const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last = prev == nsp - 1;
             if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -554,7 +633,7 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
         __syncthreads();
         if (s_last) {
             merge_any<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, reinterpret_cast<float*>(smem));
-            write_q();
+            write_q();  // every workgroup of the group has read q by now
         }
     }
 }

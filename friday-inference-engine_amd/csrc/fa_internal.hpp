@@ -17,6 +17,9 @@ namespace fa {
 constexpr int kSpan = 128;
 constexpr int kPageTokens = 16;  // paged_kv_cache.h:16 KV_BLOCK_SIZE
 constexpr int kMaxSplitsLimit = 128;
+// arrival counters of the fused merge sit 256 bytes apart, so that the atomics of
+// different head groups do not queue on one cache line
+constexpr int kCounterStride = 64;
 
 __host__ __device__ inline int split_bound(int S, int min_chunk, int max_splits) {
     int ns = S > 0 ? (S + min_chunk - 1) / min_chunk : 1;
