@@ -73,6 +73,15 @@ __device__ __forceinline__ _Float16 out_half(float r) {
 }
 
 __device__ __forceinline__ float wave_max_xor(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+
+// max of v over the lanes l, l^16, l^32, l^48 (the four lane blocks of an MFMA
+// column) with the gfx950 VALU lane swaps, no LDS round trip
+__device__ __forceinline__ float col_max4(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 __device__ __forceinline__ float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 
 // Agent-scope coherent access (global_store/load ... sc1): the store is written

@@ -18,6 +18,9 @@
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
+#include <cstdlib>
+#include <type_traits>
+
 namespace fa {
 namespace {
 
@@ -238,6 +241,352 @@ __global__ __launch_bounds__(kPfThreads) void fa_prefill_kernel(PrefillParams p)
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// fp16 caches: LDS-DMA pipeline.
+//
+// A workgroup owns RT 16-row tiles of one kv head (rows r = t*G + g) and streams the
+// head's keys in stages of 128 positions through a two-stage LDS ring that
+// global_load_lds_dwordx4 fills directly (no register staging). Each of the four
+// waves takes 32 keys of every stage for all RT row tiles, so every K/V fragment it
+// reads from LDS feeds RT MFMAs; the four waves' softmax states are merged through
+// LDS at the end. K and V rows stay row-major in LDS with the 16-byte chunks of row
+// r stored at slot chunk ^ (r % CPR), which makes the MFMA operand reads free of bank
+// conflicts; V^T comes from the transposing LDS read (ds_read_b64_tr_b16).
+constexpr int kP2Waves = 4;
+constexpr int kP2Threads = kP2Waves * 64;
+constexpr int kP2KW = 32;                   // keys per wave per stage
+constexpr int kP2KS = kP2KW * kP2Waves;     // keys per stage (128)
+constexpr float kLazy = 8.0f;               // log2 slack of the reference max (weights <= 256)
+
+template <int D>
+struct P2Geo {
+    static constexpr int ROWB = D * 2;                 // bytes of one K/V row
+    static constexpr int CPR = ROWB / 16;              // 16-byte chunks per row
+    static constexpr int RPI = 64 / CPR;               // rows per wave DMA instruction
+    static constexpr int STAGE_K = kP2KS * ROWB;       // bytes of the K (or V) part of a stage
+    static constexpr int STAGE = 2 * STAGE_K;
+    static constexpr int NI = kP2KS / RPI / kP2Waves;  // DMA instructions per wave per tensor and stage
+    static constexpr int KSTEPS = D / 32;
+    static constexpr int DTILES = D / 16;
+    static constexpr int OROW = D + 4;                 // combine row stride (floats)
+};
+
+// One wave-wide global -> LDS copy (global_load_lds_dwordx4): lane l moves 16 bytes
+// from base + off (base wave-uniform, off its own) to lds + 16*l (lds wave-uniform).
+// Issued from inline assembly: the compiler would otherwise drain every such copy before
+// any later LDS read, including reads of the other stage buffer; the kernel waits for
+// the copies itself (s_waitcnt vmcnt(0) + barrier) before reading the stage they fill.
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+__device__ __forceinline__ void dma16(const char* base, uint32_t off, lds_u8* lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off), "s"(base)
+                 : "memory");
+}
+
+template <int D, int RT>
+__global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParams p) {
+    using Gm = P2Geo<D>;
+    // two distinct stage buffers (not one array indexed by the tile's parity): the compiler
+    // then sees that the DMA into one stage does not alias the LDS reads of the other and
+    // does not drain the DMA before those reads
+    __shared__ __align__(16) unsigned char stage0[Gm::STAGE];
+    __shared__ __align__(16) unsigned char stage1[Gm::STAGE];
+
+    // grid x = kv head, y = row block (heaviest first): consecutive workgroup ids walk the
+    // kv heads, so with round-robin placement over the XCDs one kv head's blocks share an
+    // XCD and its L2 copy of K/V
+    const int kvh = blockIdx.x;
+    const int rb = gridDim.y - 1 - blockIdx.y;
+    const int R = p.T * p.G;
+    const int row0 = rb * RT * 16;
+    const int p0 = *p.d_pos0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, kb = lane >> 4;
+    const int qd = p.Hq * D;
+
+    // Q^T fragments and causal limits of this lane's rows (one per row tile)
+    h8 qf[RT][Gm::KSTEPS];
+    int lim[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r = row0 + rt * 16 + col;
+        const bool valid = r < R;
+        const int rr = valid ? r : R - 1;
+        const int t = rr / p.G, g = rr % p.G;
+        lim[rt] = valid ? p0 + t : -1;
+        const uint16_t* qrow = p.q + (size_t)t * qd + (size_t)(kvh * p.G + g) * D;
+#pragma unroll
+        for (int s = 0; s < Gm::KSTEPS; ++s) {
+            const u4 raw = *reinterpret_cast<const u4*>(qrow + s * 32 + kb * 8);
+            qf[rt][s] = *reinterpret_cast<const h8*>(&raw);
+        }
+    }
+    // settle the q loads here: the compiler would otherwise wait for them at their first
+    // use inside the stage loop, in every iteration, behind the stage copies
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int s = 0; s < Gm::KSTEPS; ++s) asm volatile("" ::"v"(qf[rt][s]));
+    const int last_row = min(row0 + RT * 16, R) - 1;
+    const int kend = p0 + last_row / p.G + 1;  // keys [0, kend) for the workgroup
+    const int ntiles = (kend + kP2KS - 1) / kP2KS;
+
+    // DMA of one stage: wave w moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K and V parts
+    const size_t rowb = (size_t)p.Hkv * Gm::ROWB;
+    const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * Gm::ROWB;
+    const char* vbase = static_cast<const char*>(p.v) + (size_t)kvh * Gm::ROWB;
+    const int drow = lane / Gm::CPR, dslot = lane % Gm::CPR;
+    // this lane's byte offsets (row, swizzled chunk) within a stage, one per DMA instruction
+    uint32_t doff[Gm::NI];
+#pragma unroll
+    for (int i = 0; i < Gm::NI; ++i) {
+        const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
+        doff[i] = (uint32_t)(r * (int)rowb + (dslot ^ (r % Gm::CPR)) * 16);
+    }
+    lds_u8* const lds0 = (lds_u8*)stage0;
+    lds_u8* const lds1 = (lds_u8*)stage1;
+    auto issue = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
+        lds_u8* st = decltype(stage_tag)::value ? lds1 : lds0;
+        // uniform base: the tile's first key
+        const size_t tile0 = (size_t)tile * kP2KS * rowb;
+        const char* kt = kbase + tile0;
+        const char* vt = vbase + tile0;
+        const int rmax = kend - 1 - tile * kP2KS;  // rows past it re-read the last key
+        if (rmax >= kP2KS - 1) {
+#pragma unroll
+            for (int i = 0; i < Gm::NI; ++i) {
+                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
+                dma16(kt, doff[i], l);
+                dma16(vt, doff[i], l + Gm::STAGE_K);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < Gm::NI; ++i) {
+                const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
+                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (dslot ^ (r % Gm::CPR)) * 16);
+                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
+                dma16(kt, off, l);
+                dma16(vt, off, l + Gm::STAGE_K);
+            }
+        }
+    };
+
+    float m_run[RT];
+    f4 o[RT][Gm::DTILES], ol[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m_run[rt] = kNegBig;
+        ol[rt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < Gm::DTILES; ++i) o[rt][i] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
+    // per row tile: first token (its rows see keys <= p0 + t_lo) and last token
+    int rt_lo[RT], rt_hi[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int r_lo = row0 + rt * 16, r_hi = min(r_lo + 15, R - 1);
+        rt_lo[rt] = r_lo < R ? p0 + r_lo / p.G : -1;
+        rt_hi[rt] = r_lo < R ? p0 + r_hi / p.G : -1;
+    }
+
+    auto step = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
+        // keep the scheduler from overlapping two stages (it would keep both stages'
+        // fragments live and spill)
+        __builtin_amdgcn_sched_barrier(0);
+        // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
+        // wave's part of the stage has landed and every wave is done with the other stage
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+
+        const unsigned char* sk = decltype(stage_tag)::value ? stage1 : stage0;
+        const unsigned char* sv = sk + Gm::STAGE_K;
+        const int wrow = wave * kP2KW;                 // first stage row of this wave's keys
+        const int kpos0 = tile * kP2KS + wrow;         // its first key position
+        // the next stage's DMA into the other buffer, in flight during this stage's compute
+        if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
+        if (kpos0 <= rt_hi[RT - 1]) {  // some row of the workgroup sees a key of this slice
+            // K fragments (A of S^T = K Q^T) for both 16-key halves, shared by all row tiles
+            h8 ka[2][Gm::KSTEPS];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int r = wrow + mt * 16 + col;
+#pragma unroll
+                for (int s = 0; s < Gm::KSTEPS; ++s)
+                    ka[mt][s] = *reinterpret_cast<const h8*>(sk + r * Gm::ROWB + (((4 * s + kb) ^ (r % Gm::CPR)) * 16));
+            }
+            // phase 1: S^T for every row tile (independent MFMA chains, no branches)
+            f4 sacc[RT][2];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    sacc[rt][mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s = 0; s < Gm::KSTEPS; ++s) sacc[rt][mt] = mfma16x16x32(ka[mt][s], qf[rt][s], sacc[rt][mt]);
+                }
+            // phase 2: online softmax in the log2 domain; lane column = row, k-slots = keys.
+            // x = score * scale * log2(e); a NaN score becomes -1e30 (fmax drops the NaN),
+            // keys in a row's future -inf (only evaluated when the slice reaches past the
+            // first row's position). The weights are taken against a reference max m_run
+            // that only moves when the row max exceeds it by more than kLazy (then the
+            // accumulators are rescaled): between moves the fp16 weights stay <= 2^kLazy.
+            float x[RT][8], mx[RT];
+            auto scores = [&](auto full_tag) __attribute__((always_inline)) {
+                constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    float m = -__builtin_inff();
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int mt = j >> 2, i = j & 3;
+                        float v = fmaxf(sacc[rt][mt][i] * p.scale2, kNegBig);
+                        if (!FULL) v = kpos0 + mt * 16 + kb * 4 + i <= lim[rt] ? v : -__builtin_inff();
+                        x[rt][j] = v;
+                        m = fmaxf(m, v);
+                    }
+                    mx[rt] = col_max4(m);
+                }
+            };
+            if (kpos0 + kP2KW - 1 <= rt_lo[0])
+                scores(std::true_type{});
+            else
+                scores(std::false_type{});
+            bool move = false;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) move |= mx[rt] > m_run[rt] + kLazy;
+            if (__any(move)) {  // rare after the first stage
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const float m_new = mx[rt] > m_run[rt] + kLazy ? mx[rt] : m_run[rt];
+                    const float alpha = exp2_fast(m_run[rt] - m_new);
+                    m_run[rt] = m_new;
+#pragma unroll
+                    for (int dt = 0; dt < Gm::DTILES; ++dt) o[rt][dt] *= alpha;
+                    ol[rt] *= alpha;
+                }
+            }
+            h8 pf[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pf[rt][j] = (_Float16)exp2_fast(x[rt][j] - m_run[rt]);
+            // V^T fragments (A of O^T += V^T P^T): k-slot j < 4 -> key kb*4 + j, j >= 4 -> 16 + kb*4 + j-4
+            h8 va[Gm::DTILES];
+            {
+                const int r = wrow + kb * 4 + (col >> 2);
+#pragma unroll
+                for (int dt = 0; dt < Gm::DTILES; ++dt) {
+                    const int d = dt * 16 + 4 * (col & 3);
+                    const unsigned char* a = sv + r * Gm::ROWB + ((((d >> 3)) ^ (r % Gm::CPR)) * 16) + (d & 7) * 2;
+                    const h4 lo = lds_read_tr16(a);
+                    const h4 hi = lds_read_tr16(a + 16 * Gm::ROWB);
+                    va[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+            // phase 4: O^T += V^T P^T, and the row sums of the fp16 weights exactly as the PV
+            // product sees them (P against a tile of ones)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+                for (int dt = 0; dt < Gm::DTILES; ++dt) o[rt][dt] = mfma16x16x32(va[dt], pf[rt], o[rt][dt]);
+                ol[rt] = mfma16x16x32(ones, pf[rt], ol[rt]);
+            }
+        }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue(0, S0{});
+    for (int tile = 0; tile < ntiles; tile += 2) {
+        step(tile, S0{});
+        if (tile + 1 < ntiles) step(tile + 1, S1{});
+    }
+
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // every wave is done reading the stages
+    // ---- merge the four waves' states (one row tile at a time through LDS) ----
+    constexpr int RB = 1;
+    float* cm = reinterpret_cast<float*>(stage0);      // [RB][kP2Waves][16]
+    float* cl = cm + RB * kP2Waves * 16;               // [RB][kP2Waves][16]
+    float* co = cl + RB * kP2Waves * 16;               // [RB][kP2Waves][16][OROW]
+    static_assert((2 * RB * kP2Waves * 16 + RB * kP2Waves * 16 * (D + 4)) * 4 <= Gm::STAGE, "combine fits");
+#pragma unroll
+    for (int rb0 = 0; rb0 < RT; rb0 += RB) {
+#pragma unroll
+        for (int k = 0; k < RB; ++k) {
+            const int rt = rb0 + k;
+            if (rt >= RT) break;
+            if (kb == 0) {
+                cm[(k * kP2Waves + wave) * 16 + col] = m_run[rt];
+                cl[(k * kP2Waves + wave) * 16 + col] = ol[rt][0];
+            }
+#pragma unroll
+            for (int dt = 0; dt < Gm::DTILES; ++dt)
+                *reinterpret_cast<f4*>(co + ((k * kP2Waves + wave) * 16 + col) * Gm::OROW + dt * 16 + kb * 4) = o[rt][dt];
+        }
+        __syncthreads();
+        const int nrt = min(RB, RT - rb0);
+        for (int idx = tid; idx < nrt * 16 * (D / 4); idx += kP2Threads) {
+            const int k = idx / (16 * (D / 4));
+            const int rem = idx % (16 * (D / 4));
+            const int rr = rem / (D / 4), d4 = rem % (D / 4);
+            const int r = row0 + (rb0 + k) * 16 + rr;
+            if (r >= R) continue;
+            float M = cm[(k * kP2Waves) * 16 + rr];
+#pragma unroll
+            for (int w = 1; w < kP2Waves; ++w) M = fmaxf(M, cm[(k * kP2Waves + w) * 16 + rr]);
+            float L = 0.0f;
+            f4 O = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < kP2Waves; ++w) {
+                const float df = cm[(k * kP2Waves + w) * 16 + rr] - M;
+                const float wt = df < kCut2 ? 0.0f : exp2_fast(df);
+                L += wt * cl[(k * kP2Waves + w) * 16 + rr];
+                O += wt * *reinterpret_cast<const f4*>(co + ((k * kP2Waves + w) * 16 + rr) * Gm::OROW + 4 * d4);
+            }
+            const int t = r / p.G, g = r % p.G;
+            h4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
+            *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(p.out) + (size_t)t * qd + (size_t)(kvh * p.G + g) * D + 4 * d4) = v;
+        }
+        __syncthreads();
+    }
+}
+
+template <int D, int RT>
+int launch_dma(const PrefillParams& p, hipStream_t stream) {
+    const int R = p.T * p.G;
+    const dim3 grid(p.Hkv, (R + RT * 16 - 1) / (RT * 16));
+    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RT>), grid, dim3(kP2Threads), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Row tiles per workgroup: about one workgroup per CU of the MI355X (256) for the
+// whole launch, at most 3 for head_dim 128 and 6 for 64 (beyond, the wave's registers
+// spill).
+template <int D>
+int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
+    static const int forced = [] {
+        const char* e = std::getenv("FRIDAY_ATTN_PREFILL_RT");
+        return e && *e ? std::atoi(e) : 0;
+    }();
+    const long rows = (long)p.T * p.G * p.Hkv;
+    int rt = forced > 0 ? forced : (int)((rows + 256 * 16 - 1) / (256 * 16));
+    const int rt_max = D == 128 ? 3 : 6;
+    if (forced <= 0 && rt > rt_max) rt = rt_max;
+    rt = rt < 1 ? 1 : (rt > 6 ? 6 : rt);
+    switch (rt) {
+        case 1: return launch_dma<D, 1>(p, stream);
+        case 2: return launch_dma<D, 2>(p, stream);
+        case 3: return launch_dma<D, 3>(p, stream);
+        case 4: return launch_dma<D, 4>(p, stream);
+        case 5: return launch_dma<D, 5>(p, stream);
+        default: return launch_dma<D, 6>(p, stream);
+    }
+}
+
 template <int D, bool Q8>
 int launch_pf(const PrefillParams& p, hipStream_t stream) {
     const int R = p.T * p.G;
@@ -249,8 +598,8 @@ int launch_pf(const PrefillParams& p, hipStream_t stream) {
 }  // namespace
 
 int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t stream) {
-    if (head_dim == 128) return q8 ? launch_pf<128, true>(p, stream) : launch_pf<128, false>(p, stream);
-    if (head_dim == 64) return q8 ? launch_pf<64, true>(p, stream) : launch_pf<64, false>(p, stream);
+    if (head_dim == 128) return q8 ? launch_pf<128, true>(p, stream) : launch_dma_rt<128>(p, stream);
+    if (head_dim == 64) return q8 ? launch_pf<64, true>(p, stream) : launch_dma_rt<64>(p, stream);
     return -2;
 }
 
