@@ -564,8 +564,7 @@ int launch_dma(const PrefillParams& p, hipStream_t stream) {
 }
 
 // Row tiles per workgroup: about one workgroup per CU of the MI355X (256) for the
-// whole launch, at most 3 for head_dim 128 and 6 for 64 (beyond, the wave's registers
-// spill).
+// whole launch, capped so that the wave's registers never spill.
 template <int D>
 int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     static const int forced = [] {
@@ -574,16 +573,17 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     }();
     const long rows = (long)p.T * p.G * p.Hkv;
     int rt = forced > 0 ? forced : (int)((rows + 256 * 16 - 1) / (256 * 16));
-    const int rt_max = D == 128 ? 3 : 6;
-    if (forced <= 0 && rt > rt_max) rt = rt_max;
-    rt = rt < 1 ? 1 : (rt > 6 ? 6 : rt);
+    // default at most 3 row tiles for head_dim 128 (measured best); 4 is the most that fits
+    // its registers without spilling
+    const int rt_max = D == 128 ? (forced > 0 ? 4 : 3) : 6;
+    rt = rt < 1 ? 1 : (rt > rt_max ? rt_max : rt);
     switch (rt) {
         case 1: return launch_dma<D, 1>(p, stream);
         case 2: return launch_dma<D, 2>(p, stream);
         case 3: return launch_dma<D, 3>(p, stream);
         case 4: return launch_dma<D, 4>(p, stream);
-        case 5: return launch_dma<D, 5>(p, stream);
-        default: return launch_dma<D, 6>(p, stream);
+        case 5: return launch_dma<D, D == 128 ? 4 : 5>(p, stream);
+        default: return launch_dma<D, D == 128 ? 4 : 6>(p, stream);
     }
 }
 
