@@ -339,7 +339,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--config", choices=("headline", "all", "others", "prefill"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other BASELINE configs")
     args = ap.parse_args()
 
@@ -364,6 +364,8 @@ def main():
         lines.append(paged_config(cx, args.steps, args.warmup))
         for rec in lines:
             print(json.dumps(rec), flush=True)
+    if args.config == "paged":
+        print(json.dumps(paged_config(cx, args.steps, args.warmup)), flush=True)
     if args.config == "prefill":
         for p0 in (0, 1024, 2048, 4096, 7680):
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup)), flush=True)

@@ -273,7 +273,8 @@ template <int D>
 constexpr int merge_lds_bytes() { return (2 * (kThreads / (D / 4)) * kMaxSplitsLimit + 64) * 4; }
 
 template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
-__global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
+// fp16 caches: two workgroups per CU (two waves per SIMD) must fit, a 256-register budget
+__global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeParams p) {
     using Gm = Geo<D, Q8>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
 
@@ -292,7 +293,8 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches on it are scalar
     const int col = lane & 15, kb = lane >> 4;
     const int g = gb * 16 + col;
     const bool gvalid = g < p.G;
@@ -330,13 +332,6 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) qcs[s * 8 + j] = cs[s * 32 + kb * 8 + j];
         }
-        const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
-        const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
-        nk = *reinterpret_cast<const u4*>(p.k_new + src + nchunk);
-        nkp = *reinterpret_cast<const u4*>(p.k_new + src + partner);
-        nv = *reinterpret_cast<const u4*>(p.v_new + src + nchunk);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ncs[j] = cs[p.neox ? (nchunk % HD2) + j : (nchunk + j) / 2];
         // the wave that loads the tile holding position S-1 (in the split holding it)
         // takes the new row from registers instead of the cache; past max_seq: no append
         const int s_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
@@ -345,6 +340,16 @@ __global__ __launch_bounds__(kThreads) void fa_decode_kernel(DecodeParams p) {
             append_wave = last_tile % kWaves;
             append_tile = last_tile;
             append_row = (S - 1) - (start + last_tile * kTile);
+        }
+        // only that wave needs the new row chunk (and its rotation partner) of its lane
+        if (wave == append_wave) {
+            const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
+            const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
+            nk = *reinterpret_cast<const u4*>(p.k_new + src + nchunk);
+            nkp = *reinterpret_cast<const u4*>(p.k_new + src + partner);
+            nv = *reinterpret_cast<const u4*>(p.v_new + src + nchunk);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ncs[j] = cs[p.neox ? (nchunk % HD2) + j : (nchunk + j) / 2];
         }
     }
 

@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         const int kpos0 = tile * kP2KS + wrow;         // its first key position
         // the next stage's DMA into the other buffer, in flight during this stage's compute
         if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
-        if (kpos0 <= rt_hi[RT - 1]) {  // some row of the workgroup sees a key of this slice
+        if (kpos0 < kend) {  // some row of the workgroup sees a key of this slice
             // K fragments (A of S^T = K Q^T) for both 16-key halves, shared by all row tiles
             h8 ka[2][Gm::KSTEPS];
 #pragma unroll
