@@ -43,7 +43,7 @@ MALL_BYTES = 256 << 20         # Infinity Cache: a "cold" working set must excee
 # HBM traffic of one step-kernel launch at the headline shape, from rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by the copy-kernel calibration
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): 135.16 MB fetched + 0.76 MB written per launch.
-HEADLINE_TRAFFIC_BYTES = 135919326
+HEADLINE_TRAFFIC_BYTES = 135924531
 
 
 def log(msg):
