@@ -287,6 +287,47 @@ def prefill_config(cx, p0, steps, warmup):
             "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "tokens_per_s": round(T / (ms * 1e-3), 0)}
 
 
+def q8_config(cx, S, L, steps, warmup):
+    """int8 KV (FRIDAY --kv q8) at the headline shape: one friday_attn_decode_step_q8 per layer."""
+    import numpy as np
+
+    fa = cx.fa
+    Hq, Hkv, d = 40, 8, 128
+    kv_dim = Hkv * d
+    lb, sb = S * kv_dim, S * (kv_dim // 32) * 2  # int8 values and fp16 scales per layer
+    k8, v8 = fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * lb)
+    ks, vs = fa.DeviceBuffer(L * sb), fa.DeviceBuffer(L * sb)
+    cx.fill(k8, L * lb // 2, 11)  # random bytes as int8 codes
+    cx.fill(v8, L * lb // 2, 12)
+    cx.fill(ks, L * sb // 2, 13, 0.02)
+    cx.fill(vs, L * sb // 2, 14, 0.02)
+    rng = np.random.default_rng(3)
+    f16 = lambda shape: rng.standard_normal(shape, dtype=np.float32).astype(np.float16).view(np.uint16)
+    q, kn, vn = (fa.DeviceBuffer.from_array(f16((L, n))) for n in (Hq * d, kv_dim, kv_dim))
+    out = fa.DeviceBuffer(L * Hq * d * 2)
+    table = fa.DeviceBuffer(fa.rope_table_bytes(S, d))
+    fa.rope_table_upload(table, S, d, 1e6)
+    pos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
+    ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, S))
+    fa.decodeWorkspaceInit(ws, stream=cx.stream.s)
+    cx.stream.synchronize()
+
+    def step():
+        for l in range(L):
+            fa.decodeStepQ8(q.ptr + l * Hq * d * 2, kn.ptr + l * kv_dim * 2, vn.ptr + l * kv_dim * 2,
+                            k8.ptr + l * lb, ks.ptr + l * sb, v8.ptr + l * lb, vs.ptr + l * sb,
+                            out.ptr + l * Hq * d * 2, pos, 0, S, Hq, Hkv, d, table, 1, ws, cx.stream.s)
+
+    ms = cx.timed(step, steps, warmup)
+    for b in (k8, v8, ks, vs, q, kn, vn, out, table, pos, ws):
+        b.free()
+    us = ms * 1e3 / L
+    nbytes = 2 * (lb + sb)
+    return {"config": "3 with int8 KV (--kv q8)", "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
+            "us_per_layer_step": round(us, 3), "kv_bytes_per_layer": nbytes, "kv_GBps": round(nbytes / us / 1e3, 1),
+            "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "tokens_per_s": round(1e6 / (us * L), 2)}
+
+
 def paged_config(cx, steps, warmup):
     """16 sequences, S ~ U[256, 16k], 16-token pages in a permuted pool, one launch."""
     import numpy as np
@@ -339,7 +380,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other BASELINE configs")
     args = ap.parse_args()
 
@@ -362,8 +403,11 @@ def main():
         for p0 in (0, 1024, 2048, 4096, 7680):
             lines.append(prefill_config(cx, p0, args.steps, args.warmup))
         lines.append(paged_config(cx, args.steps, args.warmup))
+        lines.append(q8_config(cx, 32768, 64, args.steps, args.warmup))
         for rec in lines:
             print(json.dumps(rec), flush=True)
+    if args.config == "q8":
+        print(json.dumps(q8_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
     if args.config == "paged":
         print(json.dumps(paged_config(cx, args.steps, args.warmup)), flush=True)
     if args.config == "prefill":

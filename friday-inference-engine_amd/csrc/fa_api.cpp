@@ -266,19 +266,22 @@ int friday_attn_decode_attention_fused(const uint16_t* q, const void* k_cache, c
                          num_kv_heads, head_dim, workspace, workspace_bytes, false, true, k_scale, v_scale, stream);
 }
 
-int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
-                            uint16_t* out, const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,
-                            int head_dim, const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
-                            void* stream) {
-    const char* w = "decode_step";
+namespace {
+// Shared by the fp16 and int8 one-launch steps.
+int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint16_t* v, const void* k_layer,
+                       const void* v_layer, const uint16_t* k_scale, const uint16_t* v_scale, uint16_t* out,
+                       const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads, int head_dim,
+                       const float* rope_table, int neox, void* workspace, size_t workspace_bytes, void* stream) {
     if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
     if (!q || !k || !v || !k_layer || !v_layer || !out || !rope_table || max_ctx <= 0)
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
     if (!d_pos && (pos < 0 || pos >= max_ctx))
         return fail(FA_ERR_INVALID, "%s: position %d outside [0, %d)", w, pos, max_ctx);
+    const bool q8 = k_scale != nullptr;
     const int G = num_heads / num_kv_heads;
     fa::DecodeParams p{};
     p.q = q; p.k = k_layer; p.v = v_layer; p.d_pos = d_pos; p.seq_len = d_pos ? 0 : pos + 1; p.max_seq = max_ctx;
+    p.k_scale = k_scale; p.v_scale = v_scale;
     p.out = out; p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = G; p.ngb = (G + 15) / 16;
     p.kv_dim = num_kv_heads * head_dim;
     p.min_chunk = fa::min_chunk();
@@ -293,7 +296,27 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
     if (!workspace || workspace_bytes < need)
         return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
     set_workspace(p, workspace, 1, head_dim, true);
-    return launch_status(fa::launch_decode(p, head_dim, 1, false, false, static_cast<hipStream_t>(stream)), w);
+    return launch_status(fa::launch_decode(p, head_dim, 1, false, q8, static_cast<hipStream_t>(stream)), w);
+}
+}  // namespace
+
+int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
+                            uint16_t* out, const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,
+                            int head_dim, const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    return decode_step_common("decode_step", q, k, v, k_layer, v_layer, nullptr, nullptr, out, d_pos, pos, max_ctx,
+                              num_heads, num_kv_heads, head_dim, rope_table, neox, workspace, workspace_bytes, stream);
+}
+
+int friday_attn_decode_step_q8(uint16_t* q, const uint16_t* k, const uint16_t* v, int8_t* k_layer,
+                               uint16_t* k_scale, int8_t* v_layer, uint16_t* v_scale, uint16_t* out,
+                               const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,
+                               int head_dim, const float* rope_table, int neox, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    if (!k_scale || !v_scale) return fail(FA_ERR_INVALID, "decode_step_q8: scales required");
+    return decode_step_common("decode_step_q8", q, k, v, k_layer, v_layer, k_scale, v_scale, out, d_pos, pos,
+                              max_ctx, num_heads, num_kv_heads, head_dim, rope_table, neox, workspace,
+                              workspace_bytes, stream);
 }
 
 // ---------------- prefill ----------------

@@ -32,6 +32,11 @@ constexpr int kTile = 16;  // positions per wave tile
 #define FA_DECODE_STAGES 1
 #endif
 constexpr int kStages = FA_DECODE_STAGES;  // register stages (tiles in flight) per wave
+#ifndef FA_DECODE_STAGES_Q8
+#define FA_DECODE_STAGES_Q8 2
+#endif
+// int8 rows are half as wide: twice the tiles in flight keep the same bytes in flight
+constexpr int kStagesQ8 = FA_DECODE_STAGES_Q8;
 constexpr int kShortStages = 4;            // stages when a wave has at most this many tiles
 
 template <int D, bool Q8>
@@ -66,17 +71,56 @@ __device__ __forceinline__ size_t row_index(const DecodeParams& p, int b, int po
     return (size_t)pos;
 }
 
-// Dequantize 16 int8 values with one fp16 scale into two 16-byte fp16 chunks.
+// Dequantize 16 int8 values with one fp16 scale into two 16-byte fp16 chunks. Each code
+// q becomes the fp16 number 1664 + q by splicing (q ^ 0x80) under the exponent byte
+// 0x66 (v_perm), minus 1664 (exact), times the scale: one fp16 rounding of the exact
+// product, the same bits as rounding the fp32 product q * scale to fp16.
 __device__ __forceinline__ void dequant16(u4 raw, float sc, u4& lo, u4& hi) {
-    const int8_t* c = reinterpret_cast<const int8_t*>(&raw);
-    h8 a, b;
+    const h2 s2 = h2{(_Float16)sc, (_Float16)sc};  // sc is an fp16 value: exact
+    const h2 bias = h2{(_Float16)1664.0f, (_Float16)1664.0f};
+    uint32_t o[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        a[j] = (_Float16)((float)c[j] * sc);
-        b[j] = (_Float16)((float)c[8 + j] * sc);
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u = raw[i] ^ 0x80808080u;
+        const uint32_t d0 = __builtin_amdgcn_perm(0x66666666u, u, 0x04010400u);  // bytes u0 66 u1 66
+        const uint32_t d1 = __builtin_amdgcn_perm(0x66666666u, u, 0x04030402u);  // bytes u2 66 u3 66
+        const h2 x0 = (__builtin_bit_cast(h2, d0) - bias) * s2;
+        const h2 x1 = (__builtin_bit_cast(h2, d1) - bias) * s2;
+        o[2 * i] = __builtin_bit_cast(uint32_t, x0);
+        o[2 * i + 1] = __builtin_bit_cast(uint32_t, x1);
     }
-    lo = *reinterpret_cast<u4*>(&a);
-    hi = *reinterpret_cast<u4*>(&b);
+    lo = u4{o[0], o[1], o[2], o[3]};
+    hi = u4{o[4], o[5], o[6], o[7]};
+}
+
+// int8 append of one 16-value chunk (two fp16 vectors) of a new K or V row, the lanes
+// l and l ^ 1 holding the two halves of a 32-value block (storeKvQ8Kernel,
+// cuda_math_kernels.cu:409-432): NaN -> 0, scale = fp16(amax / 127), q = clamp(rne(x /
+// scale), +-127) with the division as x * (1 / scale). Returns the 16 codes, the
+// scale as a float and its fp16 bits. All 64 lanes of the wave must call it.
+__device__ __forceinline__ void quant_chunk16(const h8* x, u4& q, float& scale, uint16_t& bits) {
+    float v[16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        float t = (float)x[e / 8][e % 8];
+        if (__builtin_isnan(t)) t = 0.0f;
+        v[e] = t;
+        amax = fmaxf(amax, fabsf(t));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    const _Float16 dh = (_Float16)(amax / 127.0f);
+    const float d = (float)dh;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    int8_t c[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int qi = (int)rintf(v[e] * inv);
+        c[e] = (int8_t)max(-127, min(127, qi));
+    }
+    q = *reinterpret_cast<const u4*>(c);
+    scale = d;
+    bits = __builtin_bit_cast(uint16_t, dh);
 }
 
 // Log-sum-exp merge of the split partials of nh consecutive query-head rows
@@ -315,14 +359,17 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
 
     // Step variant: the RoPE table entries of this lane's q fragment, and the new K/V row
     // chunk (plus its rotation partner chunk) of lane chunk `lane % CPR`, all at position
-    // S-1. They are issued before the first K/V tile and used after it is in flight.
+    // S-1. They are issued before the first K/V tile and used after it is in flight. A
+    // chunk is the 16 bytes one lane moves per cache row: 8 fp16 values, or 16 int8 ones.
     constexpr int HD2 = D / 2;
     constexpr int QCS = ROPE ? (Gm::KSTEPS / 2) * 8 : 1;  // table entries of the q fragment (neox)
+    constexpr int CW = Q8 ? 16 : 8;                       // values of one row chunk
+    constexpr int NH = ROPE ? CW / 8 : 1;                 // fp16 vectors of one row chunk
     float2 qcs[QCS];
-    u4 nk = u4{0, 0, 0, 0}, nkp = u4{0, 0, 0, 0}, nv = u4{0, 0, 0, 0};
-    float2 ncs[ROPE ? 8 : 1];
+    h8 nk[NH], nkp[NH], nv[NH];
+    float2 ncs[ROPE ? CW : 1];
     int append_wave = -1, append_tile = -1, append_row = -1;
-    const int nchunk = (lane % Gm::CPR) * 8;  // first element of this lane's fp16 row chunk
+    const int nchunk = (lane % Gm::CPR) * CW;  // first element of this lane's row chunk
     if constexpr (ROPE) {
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
@@ -345,11 +392,14 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
         if (wave == append_wave) {
             const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
             const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
-            nk = *reinterpret_cast<const u4*>(p.k_new + src + nchunk);
-            nkp = *reinterpret_cast<const u4*>(p.k_new + src + partner);
-            nv = *reinterpret_cast<const u4*>(p.v_new + src + nchunk);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ncs[j] = cs[p.neox ? (nchunk % HD2) + j : (nchunk + j) / 2];
+            for (int i = 0; i < NH; ++i) {
+                nk[i] = *reinterpret_cast<const h8*>(p.k_new + src + nchunk + 8 * i);
+                nkp[i] = *reinterpret_cast<const h8*>(p.k_new + src + partner + 8 * i);
+                nv[i] = *reinterpret_cast<const h8*>(p.v_new + src + nchunk + 8 * i);
+            }
+#pragma unroll
+            for (int j = 0; j < CW; ++j) ncs[j] = cs[p.neox ? (nchunk % HD2) + j : (nchunk + j) / 2];
         }
     }
 
@@ -358,7 +408,10 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
     // group. The new K row is rotated the same way and written to the cache by the
     // append wave; that wave substitutes the rotated row in its own tile, so it never
     // re-reads the cache row it wrote.
-    u4 rk = u4{0, 0, 0, 0};
+    // the new row as the append wave substitutes it into its tile: fp16 chunks (rk, nv[0]),
+    // or int8 chunks with their block scales (kq, ksc, vq, vsc)
+    u4 rk = u4{0, 0, 0, 0}, kq = u4{0, 0, 0, 0}, vq = u4{0, 0, 0, 0};
+    float ksc = 0.0f, vsc = 0.0f;
     auto prepare = [&]() __attribute__((always_inline)) {
         if constexpr (ROPE) {
             if (p.neox) {
@@ -386,32 +439,53 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
                     }
             }
             if (wave == append_wave) {
-                const h8 x = *reinterpret_cast<const h8*>(&nk);
-                const h8 y = *reinterpret_cast<const h8*>(&nkp);
-                h8 r;
-                if (p.neox) {
-                    const bool lo = nchunk < HD2;
+                h8 r[NH];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        _Float16 r0, r1;
-                        // pair (i, i + D/2): x0 is the low-half element
-                        rope_rotate((float)(lo ? x[j] : y[j]), (float)(lo ? y[j] : x[j]), ncs[j].x, ncs[j].y, r0, r1);
-                        r[j] = lo ? r0 : r1;
-                    }
-                } else {
+                for (int i = 0; i < NH; ++i) {
+                    const h8 x = nk[i], y = nkp[i];
+                    if (p.neox) {
+                        const bool lo = nchunk < HD2;
 #pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        _Float16 r0, r1;
-                        rope_rotate((float)x[j], (float)x[j + 1], ncs[j].x, ncs[j].y, r0, r1);
-                        r[j] = r0;
-                        r[j + 1] = r1;
+                        for (int j = 0; j < 8; ++j) {
+                            _Float16 r0, r1;
+                            const float2 c = ncs[8 * i + j];
+                            // pair (i, i + D/2): x0 is the low-half element
+                            rope_rotate((float)(lo ? x[j] : y[j]), (float)(lo ? y[j] : x[j]), c.x, c.y, r0, r1);
+                            r[i][j] = lo ? r0 : r1;
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; j += 2) {
+                            _Float16 r0, r1;
+                            const float2 c = ncs[8 * i + j];
+                            rope_rotate((float)x[j], (float)x[j + 1], c.x, c.y, r0, r1);
+                            r[i][j] = r0;
+                            r[i][j + 1] = r1;
+                        }
                     }
                 }
-                rk = *reinterpret_cast<const u4*>(&r);
-                if (lane < Gm::CPR) {
-                    const size_t dst = row_index<PAGED>(p, b, S - 1) * p.kv_dim + (size_t)kvh * D + nchunk;
-                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.k)) + dst) = rk;
-                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.v)) + dst) = nv;
+                const size_t dst = row_index<PAGED>(p, b, S - 1) * p.kv_dim + (size_t)kvh * D + nchunk;
+                if constexpr (!Q8) {
+                    rk = *reinterpret_cast<const u4*>(&r[0]);
+                    if (lane < Gm::CPR) {
+                        *reinterpret_cast<u4*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.k)) + dst) = rk;
+                        *reinterpret_cast<h8*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.v)) + dst) = nv[0];
+                    }
+                } else {
+                    // int8 cache: the rotated k (rounded to fp16 as the rope step leaves it) and
+                    // v are quantized per 32-value block (this lane's 16 values and those of
+                    // lane ^ 1) exactly as the int8 append does (storeKvQ8Kernel rules)
+                    uint16_t kbits, vbits;
+                    quant_chunk16(r, kq, ksc, kbits);
+                    quant_chunk16(nv, vq, vsc, vbits);
+                    if (lane < Gm::CPR) {
+                        *reinterpret_cast<u4*>(const_cast<char*>(static_cast<const char*>(p.k)) + dst) = kq;
+                        *reinterpret_cast<u4*>(const_cast<char*>(static_cast<const char*>(p.v)) + dst) = vq;
+                        if ((lane & 1) == 0) {
+                            const_cast<uint16_t*>(p.k_scale)[dst / 32] = kbits;
+                            const_cast<uint16_t*>(p.v_scale)[dst / 32] = vbits;
+                        }
+                    }
                 }
             }
         }
@@ -468,10 +542,18 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
             const bool live = tbase + row < end;
             if (Q8) {
                 u4 lo, hi;
-                dequant16(st.k[r], live ? st.ks[r] : 0.0f, lo, hi);
+                u4 ck = st.k[r], cv = st.v[r];
+                float sk = live ? st.ks[r] : 0.0f, sv = live ? st.vs[r] : 0.0f;
+                if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
+                    ck = kq;  // the new row, as quantized and written to the cache by this wave
+                    cv = vq;
+                    sk = ksc;
+                    sv = vsc;
+                }
+                dequant16(ck, sk, lo, hi);
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32) = lo;
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32 + 16) = hi;
-                dequant16(st.v[r], live ? st.vs[r] : 0.0f, lo, hi);
+                dequant16(cv, sv, lo, hi);
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32) = lo;
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32 + 16) = hi;
             } else {
@@ -479,7 +561,7 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
                 u4 kx = live ? st.k[r] : z, vx = live ? st.v[r] : z;
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
                     kx = rk;  // the new row, as written to the cache by this wave
-                    vx = nv;
+                    vx = *reinterpret_cast<const u4*>(&nv[0]);
                 }
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = kx;
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = vx;
@@ -510,8 +592,7 @@ __global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeP
             sc[i] = tbase + kb * 4 + i < end ? x : -__builtin_inff();
             mx = fmaxf(mx, sc[i]);
         }
-        mx = wave_max_xor(mx, 16);
-        mx = wave_max_xor(mx, 32);
+        mx = col_max4(mx);  // over the 4 lane blocks: the 16 positions of the tile
         const float m_new = fmaxf(m_run, mx);
         const float da = m_run - m_new;
         const float alpha = da < kCut2 ? 0.0f : exp2_fast(da);
@@ -658,11 +739,11 @@ template <int D, bool PAGED, bool Q8>
 int launch_t(const DecodeParams& p, int batch, hipStream_t stream) {
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
     if (p.rope_table) {
-        if (Q8 || !p.counters) return -2;  // the step needs the fused merge and fp16 caches
-        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, false, kStages, true>), grid, dim3(kThreads), 0, stream, p);
+        if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
+        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid, dim3(kThreads), 0, stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, kStages, false>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, false>), grid, dim3(kThreads), 0, stream, p);
     if (hipGetLastError() != hipSuccess) return -1;
     if (!p.single && !p.counters) {
         hipLaunchKernelGGL((fa_merge_kernel<D, PAGED>), dim3(batch * p.Hq), dim3(kThreads), 0, stream, p);

@@ -46,6 +46,8 @@ API = [
     ("friday_attn_decode_workspace_init", _I, [_P, _SZ, _P]),
     ("friday_attn_decode_attention_fused", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     ("friday_attn_decode_step", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
+    ("friday_attn_decode_step_q8", _I,
+     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_prefill_supported", _I, [_I, _I, _I]),
     ("friday_attn_prefill_attention", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P]),
     ("friday_attn_paged_workspace_bytes", _SZ, [_I, _I, _I]),
@@ -329,6 +331,17 @@ def decodeStep(q, k, v, k_layer, v_layer, out, d_pos, pos, max_ctx, num_heads, n
     _check(load().friday_attn_decode_step(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(v_layer), _ptr(out),
                                           _ptr(d_pos), pos, max_ctx, num_heads, num_kv_heads, head_dim,
                                           _ptr(rope_table), int(neox), _ptr(workspace), workspace_bytes, stream))
+
+
+def decodeStepQ8(q, k, v, k_layer, k_scale, v_layer, v_scale, out, d_pos, pos, max_ctx, num_heads, num_kv_heads,
+                 head_dim, rope_table, neox, workspace, stream=None, workspace_bytes=None):
+    """decodeStep for an int8 KV cache (values [max_ctx][Hkv*d] int8, scales [max_ctx][Hkv*d/32] fp16)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_decode_step_q8(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(k_scale), _ptr(v_layer),
+                                             _ptr(v_scale), _ptr(out), _ptr(d_pos), pos, max_ctx, num_heads,
+                                             num_kv_heads, head_dim, _ptr(rope_table), int(neox), _ptr(workspace),
+                                             workspace_bytes, stream))
 
 
 def prefillAttentionSupported(num_heads, num_kv_heads, head_dim) -> bool:

@@ -131,6 +131,19 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
                             int head_dim, const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* int8 KV cache (FRIDAY --kv q8): the same single launch as friday_attn_decode_step
+ * for the sequence transformer.cpp:1035-1040, 1049-1051 issues as three launches:
+ * ropeStoreKvKernel with null caches (q and k rotated), storeKvQ8Kernel (rotated k and
+ * v quantized into row P: int8 values plus one fp16 scale per 32 values,
+ * cuda_math_kernels.cu:409-432), then launchDecodeAttentionSplit with k_scale/v_scale.
+ * Cache layout [max_ctx][Hkv*d] int8, scales [max_ctx][Hkv*d/32] fp16. Outputs, cache
+ * row and scales are bit-identical to that sequence; k is not rotated in place. */
+int friday_attn_decode_step_q8(uint16_t* q, const uint16_t* k, const uint16_t* v, int8_t* k_layer,
+                               uint16_t* k_scale, int8_t* v_layer, uint16_t* v_scale, uint16_t* out,
+                               const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,
+                               int head_dim, const float* rope_table, int neox, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* ---------------- prefill attention ----------------
  * friday_attn::prefillAttentionSupported / launchPrefillAttention
  * (attention_kernels.h:46-50, .cu:649-684): causal attention of T queries at

@@ -131,3 +131,57 @@ def test_paged_step_matches_contiguous_step(gpu):
         assert np.array_equal(got[b], o1.download(Hq * d, np.uint16)), f"seq {b} S={S}"
         row = dkc.download((max_seq, kv_dim), np.uint16)[S - 1]
         assert np.array_equal(got_kp[table[b, (S - 1) // PAGE], (S - 1) % PAGE], row), f"k row seq {b}"
+
+
+@pytest.mark.parametrize("Hq,Hkv,d,S,max_ctx,neox,devpos", [
+    (40, 8, 128, 32768, 32768, 1, True),   # headline shape, int8 KV
+    (32, 8, 128, 1000, 1024, 0, False),    # interleaved pairs
+    (14, 2, 64, 513, 1024, 1, True),       # d = 64
+    (40, 8, 128, 1, 64, 1, True),          # first token
+])
+def test_step_q8_matches_three_launches(gpu, oracle, Hq, Hkv, d, S, max_ctx, neox, devpos):
+    """int8 KV (--kv q8): one launch == ropeStoreKv without caches + storeKvQ8 + fused split
+    decode with scales (transformer.cpp:1035-1040, 1049-1051), bit for bit, including the
+    quantized cache row and its scales; and within tolerance of the oracle."""
+    fa = gpu
+    rng = np.random.default_rng(S + 7)
+    kv_dim = Hkv * d
+    kf, vf = f16(rng, (max_ctx, kv_dim)), f16(rng, (max_ctx, kv_dim))
+    k8, v8 = np.zeros((max_ctx, kv_dim), np.int8), np.zeros((max_ctx, kv_dim), np.int8)
+    ks, vs = np.zeros((max_ctx, kv_dim // 32), np.uint16), np.zeros((max_ctx, kv_dim // 32), np.uint16)
+    oracle.store_kv_q8(kf, vf, k8, ks, v8, vs, 0, kv_dim)
+    q, k, v = f16(rng, (1, Hq * d), 2.0), f16(rng, (1, kv_dim)), f16(rng, (1, kv_dim))
+    pos = S - 1
+    table = fa.rope_table_host(max_ctx, d, 1e6)
+    dt = fa.DeviceBuffer.from_array(table)
+    dpos = fa.DeviceBuffer.from_array(np.array([pos], np.int32))
+    ws_bytes = fa.splitAttentionWorkspaceBytes(Hq, max_ctx)
+    P, pp = (dpos, 0) if devpos else (None, pos)
+
+    b1 = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q, k=k, v=v, k8=k8, ks=ks, v8=v8, vs=vs).items()}
+    out1, ws1 = fa.DeviceBuffer(q.nbytes), fa.DeviceBuffer(ws_bytes)
+    fa.decodeWorkspaceInit(ws1)
+    fa.decodeStepQ8(b1["q"], b1["k"], b1["v"], b1["k8"], b1["ks"], b1["v8"], b1["vs"], out1, P, pp, max_ctx, Hq, Hkv,
+                    d, dt, neox, ws1)
+
+    b2 = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q, k=k, v=v, k8=k8, ks=ks, v8=v8, vs=vs).items()}
+    out2, ws2 = fa.DeviceBuffer(q.nbytes), fa.DeviceBuffer(ws_bytes)
+    fa.decodeWorkspaceInit(ws2)
+    fa.ropeStoreKv(b2["q"], b2["k"], b2["v"], None, None, P, pp, 1, d, Hq, Hkv, max_ctx, dt, neox)
+    fa.storeKvQ8(b2["k"], b2["v"], b2["k8"], b2["ks"], b2["v8"], b2["vs"], P, pp, 1, kv_dim, max_ctx)
+    fa.launchDecodeAttentionFused(b2["q"], b2["k8"], b2["v8"], out2, 0 if devpos else S, P, max_ctx, Hq, Hkv, d, ws2,
+                                  k_scale=b2["ks"], v_scale=b2["vs"])
+    fa.Hip.sync()
+
+    for n, a in dict(k8=k8, ks=ks, v8=v8, vs=vs).items():
+        assert np.array_equal(b1[n].download(a.shape, a.dtype), b2[n].download(a.shape, a.dtype)), n
+    assert np.array_equal(b1["q"].download(q.shape, np.uint16), b2["q"].download(q.shape, np.uint16)), "rotated q"
+    g1, g2 = out1.download(Hq * d, np.uint16), out2.download(Hq * d, np.uint16)
+    assert np.array_equal(g1, g2), "int8 step differs from the three-launch sequence"
+    # oracle: rope (q, k), int8 append at pos, int8 decode over S
+    qr, kr, vr = q.copy(), k.copy(), v.copy()
+    oracle.rope_append(qr, kr, vr, None, None, table, pos, Hq, Hkv, d, neox)
+    oracle.store_kv_q8(kr, vr, k8, ks, v8, vs, pos, kv_dim)
+    assert np.array_equal(b1["k8"].download(k8.shape, np.int8), k8), "int8 k row vs oracle"
+    assert np.array_equal(b1["vs"].download(vs.shape, np.uint16), vs), "v scales vs oracle"
+    assert_close(as_f32(g1), oracle.decode_q8(qr[0], k8, ks, v8, vs, S, Hq, Hkv, d), f"q8 step S={S}")
