@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         const int kpos0 = tile * kP2KS + wrow;         // its first key position
         // the next stage's DMA into the other buffer, in flight during this stage's compute
         if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
-        if (kpos0 < kend) {  // some row of the workgroup sees a key of this slice
+        {  // a slice past the workgroup's last key is fully masked (zero weights)
             // K fragments (A of S^T = K Q^T) for both 16-key halves, shared by all row tiles
             h8 ka[2][Gm::KSTEPS];
 #pragma unroll
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             bool move = false;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) move |= mx[rt] > m_run[rt] + kLazy;
-            if (__any(move)) {  // rare after the first stage
+            if (__builtin_expect(__any(move), 0)) {  // rare after the first stage
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
                     const float m_new = mx[rt] > m_run[rt] + kLazy ? mx[rt] : m_run[rt];
@@ -573,17 +573,15 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     }();
     const long rows = (long)p.T * p.G * p.Hkv;
     int rt = forced > 0 ? forced : (int)((rows + 256 * 16 - 1) / (256 * 16));
-    // default at most 3 row tiles for head_dim 128 (measured best); 4 is the most that fits
-    // its registers without spilling
-    const int rt_max = D == 128 ? (forced > 0 ? 4 : 3) : 6;
+    const int rt_max = 6;
     rt = rt < 1 ? 1 : (rt > rt_max ? rt_max : rt);
     switch (rt) {
         case 1: return launch_dma<D, 1>(p, stream);
         case 2: return launch_dma<D, 2>(p, stream);
         case 3: return launch_dma<D, 3>(p, stream);
         case 4: return launch_dma<D, 4>(p, stream);
-        case 5: return launch_dma<D, D == 128 ? 4 : 5>(p, stream);
-        default: return launch_dma<D, D == 128 ? 4 : 6>(p, stream);
+        case 5: return launch_dma<D, 5>(p, stream);
+        default: return launch_dma<D, 6>(p, stream);
     }
 }
 
