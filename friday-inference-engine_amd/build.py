@@ -41,10 +41,11 @@ def _run(cmd):
     return out
 
 
-# Per-source device-compiler options. Prefill: MFMA accumulators in ordinary VGPRs. The
-# default AGPR form makes the compiler copy every accumulator between AGPRs and VGPRs at
-# every K/V stage, and inflates the register count by ~40 %.
-SOURCE_FLAGS = {"fa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source device-compiler options: MFMA accumulators in ordinary VGPRs. The default
+# AGPR form makes the compiler copy accumulators between AGPRs and VGPRs in the loops
+# (every K/V stage in prefill) and inflates the register count by up to ~40 %.
+_VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+SOURCE_FLAGS = {"fa_prefill.hip": _VGPR_MFMA, "fa_decode.hip": _VGPR_MFMA}
 
 
 def _compile(sources, ex):

@@ -317,8 +317,8 @@ template <int D>
 constexpr int merge_lds_bytes() { return (2 * (kThreads / (D / 4)) * kMaxSplitsLimit + 64) * 4; }
 
 template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
-// fp16 caches: two workgroups per CU (two waves per SIMD) must fit, a 256-register budget
-__global__ __launch_bounds__(kThreads, Q8 ? 1 : 2) void fa_decode_kernel(DecodeParams p) {
+// two workgroups per CU (two waves per SIMD) must fit: a 256-register budget
+__global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) {
     using Gm = Geo<D, Q8>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
 
