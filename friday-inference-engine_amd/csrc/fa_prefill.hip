@@ -18,6 +18,7 @@
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
+#include <climits>
 #include <cstdlib>
 #include <type_traits>
 
@@ -245,18 +246,23 @@ __global__ __launch_bounds__(kPfThreads) void fa_prefill_kernel(PrefillParams p)
 // ---------------------------------------------------------------------------
 // fp16 caches: LDS-DMA pipeline.
 //
-// A workgroup owns RT 16-row tiles of one kv head (rows r = t*G + g) and streams the
-// head's keys in stages of 128 positions through a two-stage LDS ring that
-// global_load_lds_dwordx4 fills directly (no register staging). Each of the four
-// waves takes 32 keys of every stage for all RT row tiles, so every K/V fragment it
-// reads from LDS feeds RT MFMAs; the four waves' softmax states are merged through
-// LDS at the end. K and V rows stay row-major in LDS with the 16-byte chunks of row
+// A workgroup owns RA + RB 16-row tiles of one kv head (rows r = t*G + g) and streams
+// the head's keys in stages of 128 positions through a two-stage LDS ring that
+// global_load_lds_dwordx4 fills directly (no register staging). Its eight waves form
+// two groups: group 0 holds the first RA row tiles, group 1 the next RB. Within a
+// group, each of the four waves takes 32 keys of every stage for all of the group's
+// row tiles, so every K/V fragment it reads from LDS feeds RA (or RB) MFMAs; the four
+// waves' softmax states are merged through LDS at the end. With 128 KB of LDS per
+// workgroup a CU runs one workgroup, i.e. two waves per SIMD (one of each group): while
+// one wave runs its softmax on the vector unit, the other can issue its MFMAs. K and V rows stay row-major in LDS with the 16-byte chunks of row
 // r stored at slot chunk ^ (r % CPR), which makes the MFMA operand reads free of bank
 // conflicts; V^T comes from the transposing LDS read (ds_read_b64_tr_b16).
-constexpr int kP2Waves = 4;
+constexpr int kP2Slices = 4;                // key slices of a stage (one wave each per group)
+constexpr int kP2Groups = 2;                // row-tile groups sharing every stage
+constexpr int kP2Waves = kP2Slices * kP2Groups;
 constexpr int kP2Threads = kP2Waves * 64;
 constexpr int kP2KW = 32;                   // keys per wave per stage
-constexpr int kP2KS = kP2KW * kP2Waves;     // keys per stage (128)
+constexpr int kP2KS = kP2KW * kP2Slices;    // keys per stage (128)
 constexpr float kLazy = 8.0f;               // log2 slack of the reference max (weights <= 256)
 
 template <int D>
@@ -283,12 +289,13 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t off, lds_u8* ld
                  : "memory");
 }
 
-template <int D, int RT>
+template <int D, int RA, int RB>
 __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParams p) {
     using Gm = P2Geo<D>;
+    constexpr int RT = RA;  // state arrays per lane (group 1 uses the first RB entries)
+    static_assert(RB <= RA, "group 0 holds the larger share");
     // two distinct stage buffers (not one array indexed by the tile's parity): the compiler
-    // then sees that the DMA into one stage does not alias the LDS reads of the other and
-    // does not drain the DMA before those reads
+    // then sees that the DMA into one stage does not alias the LDS reads of the other
     __shared__ __align__(16) unsigned char stage0[Gm::STAGE];
     __shared__ __align__(16) unsigned char stage1[Gm::STAGE];
 
@@ -298,12 +305,16 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     const int kvh = blockIdx.x;
     const int rb = gridDim.y - 1 - blockIdx.y;
     const int R = p.T * p.G;
-    const int row0 = rb * RT * 16;
     const int p0 = *p.d_pos0;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave / kP2Slices;  // row-tile group
+    const int sl = wave % kP2Slices;   // key slice of every stage
     const int col = lane & 15, kb = lane >> 4;
     const int qd = p.Hq * D;
+    const int wg_row0 = rb * (RA + RB) * 16;
+    const int row0 = wg_row0 + grp * RA * 16;  // the group's first row
+    const int ntl = grp == 0 ? RA : RB;        // the group's row tiles
 
     // Q^T fragments and causal limits of this lane's rows (one per row tile)
     h8 qf[RT][Gm::KSTEPS];
@@ -311,7 +322,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int r = row0 + rt * 16 + col;
-        const bool valid = r < R;
+        const bool valid = rt < ntl && r < R;
         const int rr = valid ? r : R - 1;
         const int t = rr / p.G, g = rr % p.G;
         lim[rt] = valid ? p0 + t : -1;
@@ -328,9 +339,11 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int s = 0; s < Gm::KSTEPS; ++s) asm volatile("" ::"v"(qf[rt][s]));
-    const int last_row = min(row0 + RT * 16, R) - 1;
+    const int last_row = min(wg_row0 + (RA + RB) * 16, R) - 1;
     const int kend = p0 + last_row / p.G + 1;  // keys [0, kend) for the workgroup
     const int ntiles = (kend + kP2KS - 1) / kP2KS;
+    // first token of the group's first tile: slices up to it need no causal mask
+    const int grp_lo = row0 < R ? p0 + row0 / p.G : INT_MAX;
 
     // DMA of one stage: wave w moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K and V parts
     const size_t rowb = (size_t)p.Hkv * Gm::ROWB;
@@ -382,31 +395,13 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         for (int i = 0; i < Gm::DTILES; ++i) o[rt][i] = f4{0.f, 0.f, 0.f, 0.f};
     }
     const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
-    // per row tile: first token (its rows see keys <= p0 + t_lo) and last token
-    int rt_lo[RT], rt_hi[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        const int r_lo = row0 + rt * 16, r_hi = min(r_lo + 15, R - 1);
-        rt_lo[rt] = r_lo < R ? p0 + r_lo / p.G : -1;
-        rt_hi[rt] = r_lo < R ? p0 + r_hi / p.G : -1;
-    }
+    const int wrow = sl * kP2KW;  // first stage row of this wave's keys
 
-    auto step = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
-        // keep the scheduler from overlapping two stages (it would keep both stages'
-        // fragments live and spill)
-        __builtin_amdgcn_sched_barrier(0);
-        // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
-        // wave's part of the stage has landed and every wave is done with the other stage
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-
-        const unsigned char* sk = decltype(stage_tag)::value ? stage1 : stage0;
-        const unsigned char* sv = sk + Gm::STAGE_K;
-        const int wrow = wave * kP2KW;                 // first stage row of this wave's keys
-        const int kpos0 = tile * kP2KS + wrow;         // its first key position
-        // the next stage's DMA into the other buffer, in flight during this stage's compute
-        if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
-        {  // a slice past the workgroup's last key is fully masked (zero weights)
+    // one stage's work for the group's N row tiles: S^T = K Q^T, online softmax, O^T += V^T P^T
+    auto compute = [&](auto n_tag, const unsigned char* sk, const unsigned char* sv, int kpos0)
+                       __attribute__((always_inline)) {
+        constexpr int N = decltype(n_tag)::value;
+        if constexpr (N > 0) {
             // K fragments (A of S^T = K Q^T) for both 16-key halves, shared by all row tiles
             h8 ka[2][Gm::KSTEPS];
 #pragma unroll
@@ -417,9 +412,9 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     ka[mt][s] = *reinterpret_cast<const h8*>(sk + r * Gm::ROWB + (((4 * s + kb) ^ (r % Gm::CPR)) * 16));
             }
             // phase 1: S^T for every row tile (independent MFMA chains, no branches)
-            f4 sacc[RT][2];
+            f4 sacc[N][2];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
+            for (int rt = 0; rt < N; ++rt)
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt) {
                     sacc[rt][mt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -429,14 +424,14 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             // phase 2: online softmax in the log2 domain; lane column = row, k-slots = keys.
             // x = score * scale * log2(e); a NaN score becomes -1e30 (fmax drops the NaN),
             // keys in a row's future -inf (only evaluated when the slice reaches past the
-            // first row's position). The weights are taken against a reference max m_run
-            // that only moves when the row max exceeds it by more than kLazy (then the
-            // accumulators are rescaled): between moves the fp16 weights stay <= 2^kLazy.
-            float x[RT][8], mx[RT];
+            // group's first row's position). The weights are taken against a reference max
+            // m_run that only moves when the row max exceeds it by more than kLazy (then
+            // the accumulators are rescaled): between moves the fp16 weights stay <= 2^kLazy.
+            float x[N][8], mx[N];
             auto scores = [&](auto full_tag) __attribute__((always_inline)) {
                 constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
+                for (int rt = 0; rt < N; ++rt) {
                     float m = -__builtin_inff();
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
@@ -449,16 +444,16 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     mx[rt] = col_max4(m);
                 }
             };
-            if (kpos0 + kP2KW - 1 <= rt_lo[0])
+            if (kpos0 + kP2KW - 1 <= grp_lo)
                 scores(std::true_type{});
             else
                 scores(std::false_type{});
             bool move = false;
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) move |= mx[rt] > m_run[rt] + kLazy;
+            for (int rt = 0; rt < N; ++rt) move |= mx[rt] > m_run[rt] + kLazy;
             if (__builtin_expect(__any(move), 0)) {  // rare after the first stage
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
+                for (int rt = 0; rt < N; ++rt) {
                     const float m_new = mx[rt] > m_run[rt] + kLazy ? mx[rt] : m_run[rt];
                     const float alpha = exp2_fast(m_run[rt] - m_new);
                     m_run[rt] = m_new;
@@ -467,33 +462,52 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     ol[rt] *= alpha;
                 }
             }
-            h8 pf[RT];
+            h8 pf[N];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
+            for (int rt = 0; rt < N; ++rt)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) pf[rt][j] = (_Float16)exp2_fast(x[rt][j] - m_run[rt]);
             // V^T fragments (A of O^T += V^T P^T): k-slot j < 4 -> key kb*4 + j, j >= 4 -> 16 + kb*4 + j-4
+            // (kept after the softmax: hoisted into the S phase they would not fit the registers)
+            __builtin_amdgcn_sched_barrier(0);
             h8 va[Gm::DTILES];
             {
                 const int r = wrow + kb * 4 + (col >> 2);
 #pragma unroll
                 for (int dt = 0; dt < Gm::DTILES; ++dt) {
                     const int d = dt * 16 + 4 * (col & 3);
-                    const unsigned char* a = sv + r * Gm::ROWB + ((((d >> 3)) ^ (r % Gm::CPR)) * 16) + (d & 7) * 2;
+                    const unsigned char* a = sv + r * Gm::ROWB + (((d >> 3) ^ (r % Gm::CPR)) * 16) + (d & 7) * 2;
                     const h4 lo = lds_read_tr16(a);
                     const h4 hi = lds_read_tr16(a + 16 * Gm::ROWB);
                     va[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
             }
-            // phase 4: O^T += V^T P^T, and the row sums of the fp16 weights exactly as the PV
+            // phase 3: O^T += V^T P^T, and the row sums of the fp16 weights exactly as the PV
             // product sees them (P against a tile of ones)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
+            for (int rt = 0; rt < N; ++rt) {
 #pragma unroll
                 for (int dt = 0; dt < Gm::DTILES; ++dt) o[rt][dt] = mfma16x16x32(va[dt], pf[rt], o[rt][dt]);
                 ol[rt] = mfma16x16x32(ones, pf[rt], ol[rt]);
             }
         }
+    };
+
+    auto step = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
+        // wave's part of the stage has landed and every wave is done with the other stage
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const unsigned char* sk = decltype(stage_tag)::value ? stage1 : stage0;
+        const unsigned char* sv = sk + Gm::STAGE_K;
+        // the next stage's DMA into the other buffer, in flight during this stage's compute
+        if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
+        const int kpos0 = tile * kP2KS + wrow;  // this wave's first key position
+        if (RA == RB || grp == 0)
+            compute(std::integral_constant<int, RA>{}, sk, sv, kpos0);
+        else
+            compute(std::integral_constant<int, RB>{}, sk, sv, kpos0);
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
@@ -505,66 +519,67 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // every wave is done reading the stages
-    // ---- merge the four waves' states (one row tile at a time through LDS) ----
-    constexpr int RB = 1;
-    float* cm = reinterpret_cast<float*>(stage0);      // [RB][kP2Waves][16]
-    float* cl = cm + RB * kP2Waves * 16;               // [RB][kP2Waves][16]
-    float* co = cl + RB * kP2Waves * 16;               // [RB][kP2Waves][16][OROW]
-    static_assert((2 * RB * kP2Waves * 16 + RB * kP2Waves * 16 * (D + 4)) * 4 <= Gm::STAGE, "combine fits");
+    // ---- merge the key slices' states, one row tile per group at a time through LDS ----
+    // group g uses stage buffer g: m [slices][16], l [slices][16], O [slices][16][OROW]
+    constexpr int CREG = (2 * kP2Slices * 16 + kP2Slices * 16 * Gm::OROW);  // floats per group
+    static_assert(CREG * 4 <= Gm::STAGE, "combine fits");
+    float* cm = reinterpret_cast<float*>(grp ? stage1 : stage0);
+    float* cl = cm + kP2Slices * 16;
+    float* co = cl + kP2Slices * 16;
+    const int gtid = tid % (kP2Slices * 64);
 #pragma unroll
-    for (int rb0 = 0; rb0 < RT; rb0 += RB) {
-#pragma unroll
-        for (int k = 0; k < RB; ++k) {
-            const int rt = rb0 + k;
-            if (rt >= RT) break;
+    for (int rt = 0; rt < RT; ++rt) {
+        const bool act = rt < ntl;
+        if (act) {
             if (kb == 0) {
-                cm[(k * kP2Waves + wave) * 16 + col] = m_run[rt];
-                cl[(k * kP2Waves + wave) * 16 + col] = ol[rt][0];
+                cm[sl * 16 + col] = m_run[rt];
+                cl[sl * 16 + col] = ol[rt][0];
             }
 #pragma unroll
             for (int dt = 0; dt < Gm::DTILES; ++dt)
-                *reinterpret_cast<f4*>(co + ((k * kP2Waves + wave) * 16 + col) * Gm::OROW + dt * 16 + kb * 4) = o[rt][dt];
+                *reinterpret_cast<f4*>(co + (sl * 16 + col) * Gm::OROW + dt * 16 + kb * 4) = o[rt][dt];
         }
         __syncthreads();
-        const int nrt = min(RB, RT - rb0);
-        for (int idx = tid; idx < nrt * 16 * (D / 4); idx += kP2Threads) {
-            const int k = idx / (16 * (D / 4));
-            const int rem = idx % (16 * (D / 4));
-            const int rr = rem / (D / 4), d4 = rem % (D / 4);
-            const int r = row0 + (rb0 + k) * 16 + rr;
-            if (r >= R) continue;
-            float M = cm[(k * kP2Waves) * 16 + rr];
+        if (act) {
+            for (int idx = gtid; idx < 16 * (D / 4); idx += kP2Slices * 64) {
+                const int rr = idx / (D / 4), d4 = idx % (D / 4);
+                const int r = row0 + rt * 16 + rr;
+                if (r >= R) continue;
+                float M = cm[rr];
 #pragma unroll
-            for (int w = 1; w < kP2Waves; ++w) M = fmaxf(M, cm[(k * kP2Waves + w) * 16 + rr]);
-            float L = 0.0f;
-            f4 O = f4{0.f, 0.f, 0.f, 0.f};
+                for (int w = 1; w < kP2Slices; ++w) M = fmaxf(M, cm[w * 16 + rr]);
+                float L = 0.0f;
+                f4 O = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int w = 0; w < kP2Waves; ++w) {
-                const float df = cm[(k * kP2Waves + w) * 16 + rr] - M;
-                const float wt = df < kCut2 ? 0.0f : exp2_fast(df);
-                L += wt * cl[(k * kP2Waves + w) * 16 + rr];
-                O += wt * *reinterpret_cast<const f4*>(co + ((k * kP2Waves + w) * 16 + rr) * Gm::OROW + 4 * d4);
+                for (int w = 0; w < kP2Slices; ++w) {
+                    const float df = cm[w * 16 + rr] - M;
+                    const float wt = df < kCut2 ? 0.0f : exp2_fast(df);
+                    L += wt * cl[w * 16 + rr];
+                    O += wt * *reinterpret_cast<const f4*>(co + (w * 16 + rr) * Gm::OROW + 4 * d4);
+                }
+                const int t = r / p.G, g = r % p.G;
+                h4 v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
+                *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(p.out) + (size_t)t * qd + (size_t)(kvh * p.G + g) * D + 4 * d4) = v;
             }
-            const int t = r / p.G, g = r % p.G;
-            h4 v;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
-            *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(p.out) + (size_t)t * qd + (size_t)(kvh * p.G + g) * D + 4 * d4) = v;
         }
         __syncthreads();
     }
 }
 
-template <int D, int RT>
+template <int D, int RA, int RB>
 int launch_dma(const PrefillParams& p, hipStream_t stream) {
     const int R = p.T * p.G;
-    const dim3 grid(p.Hkv, (R + RT * 16 - 1) / (RT * 16));
-    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RT>), grid, dim3(kP2Threads), 0, stream, p);
+    constexpr int rows = (RA + RB) * 16;
+    const dim3 grid(p.Hkv, (R + rows - 1) / rows);
+    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RA, RB>), grid, dim3(kP2Threads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // Row tiles per workgroup: about one workgroup per CU of the MI355X (256) for the
-// whole launch, capped so that the wave's registers never spill.
+// whole launch; group 0 takes ceil(RT/2) of them, group 1 the rest, at most three per
+// wave so that the registers of two waves per SIMD hold them.
 template <int D>
 int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     static const int forced = [] {
@@ -576,12 +591,11 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     const int rt_max = 6;
     rt = rt < 1 ? 1 : (rt > rt_max ? rt_max : rt);
     switch (rt) {
-        case 1: return launch_dma<D, 1>(p, stream);
-        case 2: return launch_dma<D, 2>(p, stream);
-        case 3: return launch_dma<D, 3>(p, stream);
-        case 4: return launch_dma<D, 4>(p, stream);
-        case 5: return launch_dma<D, 5>(p, stream);
-        default: return launch_dma<D, 6>(p, stream);
+        case 1: return launch_dma<D, 1, 0>(p, stream);
+        case 2: return launch_dma<D, 1, 1>(p, stream);
+        case 3: return launch_dma<D, 2, 1>(p, stream);
+        case 4: return launch_dma<D, 2, 2>(p, stream);
+        default: return launch_dma<D, 3, 3>(p, stream);  // 5 as well: (3,2) spills
     }
 }
 
