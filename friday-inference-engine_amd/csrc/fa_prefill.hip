@@ -257,19 +257,13 @@ __global__ __launch_bounds__(kPfThreads) void fa_prefill_kernel(PrefillParams p)
 // one wave runs its softmax on the vector unit, the other can issue its MFMAs. K and V rows stay row-major in LDS with the 16-byte chunks of row
 // r stored at slot chunk ^ (r % CPR), which makes the MFMA operand reads free of bank
 // conflicts; V^T comes from the transposing LDS read (ds_read_b64_tr_b16).
-#ifndef FA_PF_DMA_WAVES
-#define FA_PF_DMA_WAVES 4  // waves that issue the stage copies (8: all, 4: group 0)
-#endif
-#ifndef FA_PF_FMA
-#define FA_PF_FMA 1
-#endif
-#ifndef FA_PF_SETPRIO
-#define FA_PF_SETPRIO 0  // raise the wave priority over its MFMA phases
-#endif
 constexpr int kP2Slices = 4;                // key slices of a stage (one wave each per group)
 constexpr int kP2Groups = 2;                // row-tile groups sharing every stage
 constexpr int kP2Waves = kP2Slices * kP2Groups;
 constexpr int kP2Threads = kP2Waves * 64;
+// Group 0 issues every stage copy: it starts a stage behind group 1, whose QK MFMAs and
+// softmax then overlap group 0's copy issue, which waits on the memory pipeline.
+constexpr int kP2DmaWaves = kP2Slices;
 constexpr int kP2KW = 32;                   // keys per wave per stage
 constexpr int kP2KS = kP2KW * kP2Slices;    // keys per stage (128)
 constexpr float kLazy = 8.0f;               // log2 slack of the reference max (weights <= 256)
@@ -281,7 +275,7 @@ struct P2Geo {
     static constexpr int RPI = 64 / CPR;               // rows per wave DMA instruction
     static constexpr int STAGE_K = kP2KS * ROWB;       // bytes of the K (or V) part of a stage
     static constexpr int STAGE = 2 * STAGE_K;
-    static constexpr int NI = kP2KS / RPI / FA_PF_DMA_WAVES;  // DMA instructions per wave per tensor and stage
+    static constexpr int NI = kP2KS / RPI / kP2DmaWaves;  // DMA instructions per wave per tensor and stage
     static constexpr int KSTEPS = D / 32;
     static constexpr int DTILES = D / 16;
     static constexpr int OROW = D + 4;                 // combine row stride (floats)
@@ -369,7 +363,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     lds_u8* const lds0 = (lds_u8*)stage0;
     lds_u8* const lds1 = (lds_u8*)stage1;
     auto issue = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
-        if (FA_PF_DMA_WAVES < kP2Waves && wave >= FA_PF_DMA_WAVES) return;
+        if (wave >= kP2DmaWaves) return;
         lds_u8* st = decltype(stage_tag)::value ? lds1 : lds0;
         // uniform base: the tile's first key
         const size_t tile0 = (size_t)tile * kP2KS * rowb;
@@ -422,9 +416,6 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     ka[mt][s] = *reinterpret_cast<const h8*>(sk + r * Gm::ROWB + (((4 * s + kb) ^ (r % Gm::CPR)) * 16));
             }
             // phase 1: S^T for every row tile (independent MFMA chains, no branches)
-#if FA_PF_SETPRIO
-            __builtin_amdgcn_s_setprio(1);
-#endif
             f4 sacc[N][2];
 #pragma unroll
             for (int rt = 0; rt < N; ++rt)
@@ -435,14 +426,12 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     for (int s = 0; s < Gm::KSTEPS; ++s) sacc[rt][mt] = mfma16x16x32(ka[mt][s], qf[rt][s], sacc[rt][mt]);
                 }
             // phase 2: online softmax in the log2 domain; lane column = row, k-slots = keys.
-            // x = score * scale * log2(e); a NaN score becomes -1e30 (fmax drops the NaN),
-            // keys in a row's future -inf (only evaluated when the slice reaches past the
-            // group's first row's position). The weights are taken against a reference max
+            // x = raw score (its scale, scale * log2(e), is applied in the max and the weight
+            // FMA); keys in a row's future -inf (only evaluated when the slice reaches past the
+            // group's first row's position); the row max drops NaN scores, which then count as
+            // -1e30 after scaling. The weights are taken against a reference max
             // m_run that only moves when the row max exceeds it by more than kLazy (then
             // the accumulators are rescaled): between moves the fp16 weights stay <= 2^kLazy.
-#if FA_PF_SETPRIO
-            __builtin_amdgcn_s_setprio(0);
-#endif
             float x[N][8], mx[N];
             auto scores = [&](auto full_tag) __attribute__((always_inline)) {
                 constexpr bool FULL = decltype(full_tag)::value;
@@ -452,24 +441,17 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const int mt = j >> 2, i = j & 3;
-#if FA_PF_FMA
                         float v = sacc[rt][mt][i];
-#else
-                        float v = fmaxf(sacc[rt][mt][i] * p.scale2, kNegBig);
-#endif
                         if (!FULL) v = kpos0 + mt * 16 + kb * 4 + i <= lim[rt] ? v : -__builtin_inff();
                         x[rt][j] = v;
                         m = fmaxf(m, v);
                     }
-#if FA_PF_FMA
                     // max(s) * scale2 == max(s * scale2) exactly (scale2 > 0, rounding is monotone)
                     mx[rt] = fmaxf(col_max4(m) * p.scale2, kNegBig);
-#else
-                    mx[rt] = col_max4(m);
-#endif
                 }
             };
-            if (kpos0 + kP2KW - 1 <= grp_lo)
+            const bool full = kpos0 + kP2KW - 1 <= grp_lo;
+            if (full)
                 scores(std::true_type{});
             else
                 scores(std::false_type{});
@@ -487,15 +469,24 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     ol[rt] *= alpha;
                 }
             }
+            // weights exp2(s * scale2 - m_run) in one FMA. A NaN score counts as a scaled
+            // score of -1e30: its exponent is clamped to -1e30 - m_run (weight 1 while no
+            // finite score has moved m_run off -1e30, else 0); masked keys get weight 0.
             h8 pf[N];
 #pragma unroll
-            for (int rt = 0; rt < N; ++rt)
+            for (int rt = 0; rt < N; ++rt) {
+                const float nb = kNegBig - m_run[rt];
 #pragma unroll
-#if FA_PF_FMA
-                for (int j = 0; j < 8; ++j) pf[rt][j] = (_Float16)exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), kNegBig));
-#else
-                for (int j = 0; j < 8; ++j) pf[rt][j] = (_Float16)exp2_fast(x[rt][j] - m_run[rt]);
-#endif
+                for (int j = 0; j < 8; ++j)
+                    pf[rt][j] = (_Float16)exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), nb));
+            }
+            if (!full) {
+#pragma unroll
+                for (int rt = 0; rt < N; ++rt)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (x[rt][j] == -__builtin_inff()) pf[rt][j] = (_Float16)0.0f;
+            }
             // V^T fragments (A of O^T += V^T P^T): k-slot j < 4 -> key kb*4 + j, j >= 4 -> 16 + kb*4 + j-4
             // (kept after the softmax: hoisted into the S phase they would not fit the registers)
             __builtin_amdgcn_sched_barrier(0);
@@ -513,18 +504,12 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             }
             // phase 3: O^T += V^T P^T, and the row sums of the fp16 weights exactly as the PV
             // product sees them (P against a tile of ones)
-#if FA_PF_SETPRIO
-            __builtin_amdgcn_s_setprio(1);
-#endif
 #pragma unroll
             for (int rt = 0; rt < N; ++rt) {
 #pragma unroll
                 for (int dt = 0; dt < Gm::DTILES; ++dt) o[rt][dt] = mfma16x16x32(va[dt], pf[rt], o[rt][dt]);
                 ol[rt] = mfma16x16x32(ones, pf[rt], ol[rt]);
             }
-#if FA_PF_SETPRIO
-            __builtin_amdgcn_s_setprio(0);
-#endif
         }
     };
 

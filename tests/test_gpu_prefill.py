@@ -103,3 +103,25 @@ def test_single_token_first_position(gpu):
     got = run_prefill(fa, q, k, v, None, None, 1, 0, Hq, Hkv, d)
     exp = np.concatenate([as_f32(v[0, (h // 4) * d:(h // 4 + 1) * d]) for h in range(Hq)])
     assert np.array_equal(got[0], exp)
+
+
+@pytest.mark.parametrize("d,q8", [(128, False), (64, False), (128, True)])
+def test_nan_scores(gpu, oracle, d, q8):
+    """A NaN score becomes -1e30 (attention.cu NaN rule, as in decode): a NaN K row is
+    excluded, and a token whose q is all NaN sees every score at -1e30 -> uniform weights
+    over its visible keys (mean of V). Several stages, NaN rows before and inside the chunk."""
+    fa = gpu
+    Hq, Hkv, T, p0 = 40, 8, 300, 200
+    rng = np.random.default_rng(77 + d)
+    q = f16(rng, (T, Hq * d))
+    k, v, ks, vs = make_cache(rng, p0 + T, Hkv * d, q8)
+    nan16 = np.float16(np.nan).view(np.uint16)
+    if not q8:
+        k[50, :] = nan16
+        k[p0 + 10, :] = nan16
+    for t in (0, 3, 130, 299):
+        q[t, :] = nan16
+    got = run_prefill(fa, q, k, v, ks, vs, T, p0, Hq, Hkv, d)
+    ref = oracle.prefill_q8(q, k, ks, v, vs, T, p0, Hq, Hkv, d) if q8 else oracle.prefill(q, k, v, T, p0, Hq, Hkv, d)
+    assert np.isfinite(got).all()
+    assert_close(got, ref, f"prefill NaN d{d} q8={q8}")
