@@ -77,6 +77,18 @@ void or_prefill_attention_q8(const uint16_t* q, const int8_t* k_cache, const uin
  * Gathers positions [0, S) into a contiguous [S][kv_dim] buffer. */
 void or_paged_gather(const uint16_t* pool, const int32_t* block_table, int S, int page, int kv_dim, uint16_t* dst);
 
+/* ---- prefill projection GEMM (gemm_oracle.c); kind = friday_hpc::Q8Kind code 1..6 ---- */
+size_t or_q8_row_bytes(int kind, int K);
+/* x [rows][K] fp16 -> xq [rows][K] int8, xd [rows][K/32] fp32 */
+void or_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd);
+/* 32-value block blk of a weight row: value l = ws[l/16] * q[l] - wm[l/16] */
+int or_kq_block(int kind, const uint8_t* row, int blk, int32_t* q, float* ws, float* wm);
+void or_dequant_row(int kind, const uint8_t* row, int K, float* out);
+/* Y[t*ldy + n] (fp16, epilogue with optional bias[N] and res (same layout as Y));
+ * yraw [T][N] (optional) gets the fp32 sums before the epilogue */
+void or_gemm_q8(int kind, const uint8_t* W, const int8_t* xq, const float* xd, int T, int K, int N,
+                const float* bias, const uint16_t* res, int ldy, uint16_t* Y, float* yraw);
+
 #ifdef __cplusplus
 }
 #endif

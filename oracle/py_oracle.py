@@ -24,6 +24,7 @@ _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i = C.c_int
 
 
@@ -59,6 +60,14 @@ class Oracle:
         L.or_prefill_attention.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_prefill_attention_q8.argtypes = [_u16p, _i8p, _u16p, _i8p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_paged_gather.argtypes = [_u16p, _i32p, _i, _i, _i, _u16p]
+        L.or_q8_row_bytes.restype = C.c_size_t
+        L.or_q8_row_bytes.argtypes = [_i, _i]
+        L.or_quantize_q8_rows.argtypes = [_u16p, _i, _i, _i8p, _f32p]
+        L.or_kq_block.restype = _i
+        L.or_kq_block.argtypes = [_i, _u8p, _i, _i32p, _f32p, _f32p]
+        L.or_dequant_row.argtypes = [_i, _u8p, _i, _f32p]
+        L.or_gemm_q8.argtypes = [_i, _u8p, _i8p, _f32p, _i, _i, _i, C.c_void_p, C.c_void_p, _i, C.c_void_p,
+                                 C.c_void_p]
 
     # fp16
     def h2f(self, h) -> np.ndarray:
@@ -148,6 +157,45 @@ class Oracle:
         return dst
 
 
+    # prefill projection GEMM (kind = friday_hpc::Q8Kind code: 1 Q2_K .. 5 Q6_K, 6 Q8_0)
+    def q8_row_bytes(self, kind, K) -> int:
+        return int(self.lib.or_q8_row_bytes(kind, K))
+
+    def quantize_q8_rows(self, x):
+        x = _f16bits(x)
+        rows, K = x.shape
+        xq = np.empty((rows, K), np.int8)
+        xd = np.empty((rows, K // 32), np.float32)
+        self.lib.or_quantize_q8_rows(x.ravel(), rows, K, xq.ravel(), xd.ravel())
+        return xq, xd
+
+    def kq_block(self, kind, row, blk):
+        q = np.empty(32, np.int32)
+        ws = np.empty(2, np.float32)
+        wm = np.empty(2, np.float32)
+        assert self.lib.or_kq_block(kind, np.ascontiguousarray(row, np.uint8), blk, q, ws, wm) == 0
+        return q, ws, wm
+
+    def dequant_row(self, kind, row, K) -> np.ndarray:
+        out = np.empty(K, np.float32)
+        self.lib.or_dequant_row(kind, np.ascontiguousarray(row, np.uint8), K, out)
+        return out
+
+    def gemm_q8(self, kind, W, xq, xd, T, K, N, bias=None, res=None, ldy=None):
+        """Returns (Y fp16 bits [T][ldy], fp32 sums before the epilogue [T][N])."""
+        ldy = N if ldy is None else ldy
+        W = np.ascontiguousarray(W, np.uint8)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        r = None if res is None else _f16bits(res).copy()
+        Y = np.zeros((T, ldy), np.uint16)
+        raw = np.empty((T, N), np.float32)
+        self.lib.or_gemm_q8(kind, W.ravel(), np.ascontiguousarray(xq, np.int8).ravel(),
+                            np.ascontiguousarray(xd, np.float32).ravel(), T, K, N,
+                            None if b is None else b.ctypes.data, None if r is None else r.ctypes.data, ldy,
+                            Y.ctypes.data, raw.ctypes.data)
+        return Y, raw
+
+
 class RefCpu:
     """The reference's own CPU functions (cpu_ops.cpp), compiled from source."""
 
@@ -164,6 +212,11 @@ class RefCpu:
         L.ref_decode_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _i]
         L.ref_pool_size.restype = _i
         L.ref_pool_size.argtypes = [_i]
+        L.ref_quantize_activation.argtypes = [_f32p, _i, _i8p, _f32p]
+        L.ref_dequantize_row.restype = _i
+        L.ref_dequantize_row.argtypes = [C.c_char_p, _u8p, _f32p, _i]
+        L.ref_gemv_rows_scalar.argtypes = [C.c_char_p, _u8p, _f32p, _i, _f32p, _i, _i]
+        L.ref_gemv_rows.argtypes = [C.c_char_p, _u8p, _f32p, _i, _f32p, _i, _i]
 
     def rope(self, q, k, head_dim, nq, nk, pos, base, neox, freq_factors=None):
         ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
@@ -175,6 +228,31 @@ class RefCpu:
                                       np.ascontiguousarray(kc, np.float32).ravel(),
                                       np.ascontiguousarray(vc, np.float32).ravel(), out, seq, Hq, Hkv, d, threads)
         return out
+
+    def quantize_activation(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        K = x.size
+        q = np.empty(K, np.int8)
+        d = np.empty(K // 32, np.float32)
+        self.lib.ref_quantize_activation(x, K, q, d)
+        return q, d
+
+    def dequantize_row(self, dtype, row, K) -> np.ndarray:
+        out = np.empty(K, np.float32)
+        assert self.lib.ref_dequantize_row(dtype.encode(), np.ascontiguousarray(row, np.uint8), out, K) == 1
+        return out
+
+    def gemv_rows_scalar(self, dtype, W, x, K, N) -> np.ndarray:
+        y = np.zeros(N, np.float32)
+        self.lib.ref_gemv_rows_scalar(dtype.encode(), np.ascontiguousarray(W, np.uint8).ravel(),
+                                      np.ascontiguousarray(x, np.float32), K, y, 0, N)
+        return y
+
+    def gemv_rows(self, dtype, W, x, K, r0, r1, y=None) -> np.ndarray:
+        y = np.zeros(r1, np.float32) if y is None else y
+        self.lib.ref_gemv_rows(dtype.encode(), np.ascontiguousarray(W, np.uint8).ravel(),
+                               np.ascontiguousarray(x, np.float32), K, y, r0, r1)
+        return y
 
 
 def ref_available() -> bool:

@@ -42,4 +42,35 @@ void ref_decode_attention(const float* q, const float* k_cache, const float* v_c
 
 int ref_pool_size(int threads) { return pool(threads).size(); }
 
+// cpu_kquants.cpp:75-139: x [K] fp32 -> q [K] int8, d [K/32]
+void ref_quantize_activation(const float* x, int K, int8_t* q, float* d) {
+    friday_cpu::Q8Activation a;
+    friday_cpu::quantizeActivation(x, K, a);
+    for (int i = 0; i < K; ++i) q[i] = a.q[i];
+    for (int i = 0; i < K / 32; ++i) d[i] = a.d[i];
+}
+
+// cpu_kquants.cpp:227-280 for a GGUF dtype name ("Q2_K" ...); 0 if unsupported
+int ref_dequantize_row(const char* dtype, const uint8_t* row, float* out, int dim) {
+    return friday_cpu::dequantizeRow(dtype, row, out, dim) ? 1 : 0;
+}
+
+// cpu_kquants.cpp:437-455: y[r] = gemvRowsScalar row r against x quantised by quantizeActivation
+void ref_gemv_rows_scalar(const char* dtype, const uint8_t* W, const float* x, int K, float* y, int r0, int r1) {
+    friday_cpu::KQuant t;
+    if (!friday_cpu::kquantFromDtype(dtype, &t)) return;
+    friday_cpu::Q8Activation a;
+    friday_cpu::quantizeActivation(x, K, a);
+    friday_cpu::gemvRowsScalar(t, W, a, y, r0, r1);
+}
+
+// cpu_kquants.cpp:688-: the default (AVX2 when the host has it) row GEMV, timed as the CPU baseline
+void ref_gemv_rows(const char* dtype, const uint8_t* W, const float* x, int K, float* y, int r0, int r1) {
+    friday_cpu::KQuant t;
+    if (!friday_cpu::kquantFromDtype(dtype, &t)) return;
+    friday_cpu::Q8Activation a;
+    friday_cpu::quantizeActivation(x, K, a);
+    friday_cpu::gemvRows(t, W, a, y, r0, r1);
+}
+
 }  // extern "C"
