@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libfriday_attn.so")
-SOURCES = ["fa_api.cpp", "fa_append.hip", "fa_decode.hip", "fa_prefill.hip"]
+SOURCES = ["fa_api.cpp", "fa_append.hip", "fa_decode.hip", "fa_prefill.hip", "kq_gemm.hip"]
 # benchmark-only helpers (synthetic fill, calibration copy), a separate library
 BENCHKIT_SOURCES = ["fa_benchkit.hip"]
 BENCHKIT = os.path.join(LIB_DIR, "libfa_benchkit.so")
@@ -45,7 +45,7 @@ def _run(cmd):
 # AGPR form makes the compiler copy accumulators between AGPRs and VGPRs in the loops
 # (every K/V stage in prefill) and inflates the register count by up to ~40 %.
 _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-SOURCE_FLAGS = {"fa_prefill.hip": _VGPR_MFMA, "fa_decode.hip": _VGPR_MFMA}
+SOURCE_FLAGS = {"fa_prefill.hip": _VGPR_MFMA, "fa_decode.hip": _VGPR_MFMA, "kq_gemm.hip": _VGPR_MFMA}
 
 
 def _compile(sources, ex):

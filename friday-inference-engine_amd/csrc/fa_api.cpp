@@ -417,4 +417,46 @@ int friday_attn_paged_decode_attention(const uint16_t* q, const uint16_t* k_pool
                                nullptr, 0, workspace, workspace_bytes, stream);
 }
 
+// ---------------- prefill projection GEMM ----------------
+
+static bool kq_kind_ok(int kind) { return kind >= FA_KQ_Q2_K && kind <= FA_KQ_Q8_0; }
+
+size_t friday_q8_row_bytes(int kind, int K) {
+    if (!kq_kind_ok(kind) || K <= 0) return 0;
+    static const int sb_bytes[7] = {0, 84, 110, 144, 176, 210, 0};
+    if (kind == FA_KQ_Q8_0) return K % 32 ? 0 : (size_t)(K / 32) * 34;
+    return K % 256 ? 0 : (size_t)(K / 256) * sb_bytes[kind];
+}
+
+int friday_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd, void* stream) {
+    const char* w = "quantize_q8_rows";
+    if (rows <= 0) return ok();
+    if (K <= 0 || K % 32) return fail(FA_ERR_INVALID, "%s: K must be a positive multiple of 32 (got %d)", w, K);
+    if (!x || !xq || !xd) return fail(FA_ERR_INVALID, "%s: null argument", w);
+    if (rows > 65535) return fail(FA_ERR_UNSUPPORTED, "%s: at most 65535 rows per call (got %d)", w, rows);
+    return launch_status(fa::launch_quantize_q8_rows(x, rows, K, xq, xd, static_cast<hipStream_t>(stream)), w);
+}
+
+int friday_gemm_q8_supported(int kind, int K) { return kq_kind_ok(kind) && K > 0 && K % 256 == 0 ? 1 : 0; }
+
+int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
+                   int ldy, void* stream, const float* bias, const uint16_t* res) {
+    const char* w = "gemm_q8";
+    if (!friday_gemm_q8_supported(kind, K))
+        return fail(FA_ERR_UNSUPPORTED, "%s: unsupported type %d or K=%d (K must be a multiple of 256)", w, kind, K);
+    if (T <= 0) return ok();
+    if (N <= 0 || ldy < N) return fail(FA_ERR_INVALID, "%s: invalid N=%d / ldy=%d", w, N, ldy);
+    if (!W || !xq || !xd || !Y) return fail(FA_ERR_INVALID, "%s: null argument", w);
+    if (reinterpret_cast<uintptr_t>(W) % 4 || reinterpret_cast<uintptr_t>(xq) % 16 ||
+        reinterpret_cast<uintptr_t>(xd) % 4 || reinterpret_cast<uintptr_t>(Y) % 2)
+        return fail(FA_ERR_INVALID, "%s: misaligned W (4 B), xq (16 B), xd or Y", w);
+    const long long blocks = (long long)((N + 127) / 128 + 7) / 8 * 8 * ((T + 127) / 128);
+    if (blocks > 0x7fffffffLL) return fail(FA_ERR_UNSUPPORTED, "%s: T=%d x N=%d too large for one launch", w, T, N);
+    fa::KqGemmParams p{};
+    p.W = static_cast<const uint8_t*>(W); p.xq = xq; p.xd = xd; p.Y = Y; p.bias = bias; p.res = res;
+    p.row_bytes = friday_q8_row_bytes(kind, K);
+    p.T = T; p.K = K; p.N = N; p.ldy = ldy;
+    return launch_status(fa::launch_kq_gemm(kind, p, static_cast<hipStream_t>(stream)), w);
+}
+
 }  // extern "C"

@@ -118,4 +118,19 @@ struct PrefillParams {
 
 int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t stream);
 
+// Prefill projection GEMM (kq_gemm.hip). Weight kinds: the codes of friday_hpc::Q8Kind.
+enum KqKind { kKqQ2K = 1, kKqQ3K = 2, kKqQ4K = 3, kKqQ5K = 4, kKqQ6K = 5, kKqQ80 = 6 };
+struct KqGemmParams {
+    const uint8_t* W;      // [N][row_bytes] GGML blocks
+    const int8_t* xq;      // [T][K]
+    const float* xd;       // [T][K / 32]
+    uint16_t* Y;           // row t at Y + t * ldy (fp16)
+    const float* bias;     // [N] or null
+    const uint16_t* res;   // same layout as Y, or null (may alias Y)
+    size_t row_bytes;
+    int T, K, N, ldy;
+};
+int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream);
+int launch_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd, hipStream_t stream);
+
 }  // namespace fa

@@ -56,6 +56,10 @@ API = [
      [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_paged_decode_attention", _I,
      [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    ("friday_q8_row_bytes", _SZ, [_I, _I]),
+    ("friday_quantize_q8_rows", _I, [_P, _I, _I, _P, _P, _P]),
+    ("friday_gemm_q8_supported", _I, [_I, _I]),
+    ("friday_gemm_q8", _I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _P]),
 ]
 
 _lib = None
@@ -386,3 +390,25 @@ def launchPagedDecodeAttention(q, k_pool, v_pool, out, block_table, block_table_
                                                      _ptr(block_table), block_table_stride, _ptr(seq_lens), batch,
                                                      max_seq_len, num_heads, num_kv_heads, head_dim,
                                                      _ptr(workspace), workspace_bytes, stream))
+
+
+# ---- prefill projection GEMM (friday_prefill::gemmQ8, friday_hpc::quantizeQ8Rows) ----
+# weight kinds: the codes of friday_hpc::Q8Kind
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0 = 1, 2, 3, 4, 5, 6
+
+
+def q8RowBytes(kind, K) -> int:
+    return load().friday_q8_row_bytes(kind, K)
+
+
+def quantizeQ8Rows(x, rows, K, xq, xd, stream=None):
+    _check(load().friday_quantize_q8_rows(_ptr(x), rows, K, _ptr(xq), _ptr(xd), stream))
+
+
+def gemmQ8Supported(kind, K) -> bool:
+    return bool(load().friday_gemm_q8_supported(kind, K))
+
+
+def gemmQ8(kind, W, xq, xd, T, K, N, Y, ldy, stream=None, bias=None, res=None):
+    _check(load().friday_gemm_q8(kind, _ptr(W), _ptr(xq), _ptr(xd), T, K, N, _ptr(Y), ldy, stream, _ptr(bias),
+                                 _ptr(res)))

@@ -184,6 +184,37 @@ int friday_attn_paged_decode_attention(const uint16_t* q, const uint16_t* k_pool
                                        int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
                                        void* stream);
 
+/* ---------------- prefill projection GEMM (int8 activations x K-quant weights) ----------------
+ * The batched matmul on either side of prefill attention in prefillLayerFused
+ * (transformer.cpp:1194-1207, 1266-1280). Weight kinds are the codes of
+ * friday_hpc::Q8Kind (hpc_k_quants.h:39); W holds N rows in the GGML block layout of the
+ * kind (row bytes = friday_q8_row_bytes(kind, K)). */
+#define FA_KQ_Q2_K 1
+#define FA_KQ_Q3_K 2
+#define FA_KQ_Q4_K 3
+#define FA_KQ_Q5_K 4
+#define FA_KQ_Q6_K 5
+#define FA_KQ_Q8_0 6
+size_t friday_q8_row_bytes(int kind, int K);
+/* Replaces friday_hpc::quantizeQ8Rows (hpc_k_quants.h:58-61, hpc_k_quants.cu:898-901):
+ * x [rows][K] fp16 -> xq [rows][K] int8, xd [rows][K/32] fp32; per 32 values
+ * d = amax / 127, q = clamp(rne(x / d), +-127), exactly as quantize_x_q8_kernel
+ * (hpc_k_quants.cu:386-400). K must be a multiple of 32. */
+int friday_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd, void* stream);
+/* Replaces friday_prefill::gemmQ8Supported (prefill_kernels.h:17-18, prefill_kernels.cu:340):
+ * 1 / 0. K must be a multiple of 256. */
+int friday_gemm_q8_supported(int kind, int K);
+/* Replaces friday_prefill::gemmQ8 (prefill_kernels.h:20-25, prefill_kernels.cu:342-362):
+ * Y[t*ldy + n] = sum_k W[n][k] x_t[k] for t < T, n < N, x_t = xq row t scaled by xd per
+ * 32 values; epilogue per element as storeY (prefill_kernels.cu:155-171): fp16 rounding,
+ * then + bias[n] (fp32) if bias, then res[t*ldy + n] + y (fp16) if res; NaN inputs of
+ * each sum count as 0 and sums clamp to +-65504. Y may alias res. T <= 0 is a no-op.
+ * W must be 4-byte aligned, xq 16-byte aligned, ldy >= N. Runs on gfx950 fp16 MFMA over
+ * operands decoded in LDS; agrees with the reference's integer form within its own GEMM
+ * test bar (test_prefill_gemm.cu:111-129: rel-L2 < 1e-3, max |diff| < 1e-2 RMS). */
+int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
+                   int ldy, void* stream, const float* bias, const uint16_t* res);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,7 +7,8 @@
  *   or_quantize_q8_rows   quantize_x_q8_kernel, hpc_k_quants.cu:386-400 (and the
  *                         CPU twin quantizeActivation, cpu_kquants.cpp:75-139):
  *                         per 32 values d = amax / 127 (fp32), inv = d > 0 ? 1/d : 0,
- *                         q = clamp(rne(x * inv), +-127)
+ *                         q = clamp(rne(x * inv), +-127), a NaN product -> 0 (CUDA's
+ *                         float -> int conversion; the CPU twin leaves it undefined)
  *   or_dequant_row        dequantizeRow, cpu_kquants.cpp:227-280 (fp32 formulas)
  *   or_kq_block           the integer form of one 32-value block of a weight row,
  *                         dequant32 in prefill_kernels.cu:57-144: integers q, the
@@ -31,6 +32,7 @@
 #include "fa_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 enum { KQ2 = 1, KQ3 = 2, KQ4 = 3, KQ5 = 4, KQ6 = 5, KQ80 = 6 };
@@ -65,7 +67,10 @@ void or_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* 
             const float d = amax / 127.0f;
             const float inv = d > 0.0f ? 1.0f / d : 0.0f;
             for (int i = 0; i < 32; ++i) {
-                int q = (int)nearbyintf(or_half_to_float(p[i]) * inv);
+                /* __float2int_rn of a NaN product (inf * 0, NaN input) is 0; C leaves
+                 * (int) of NaN undefined, so it is spelled out */
+                const float y = or_half_to_float(p[i]) * inv;
+                int q = isnan(y) ? 0 : (int)nearbyintf(y);
                 q = q < -127 ? -127 : (q > 127 ? 127 : q);
                 xq[(size_t)r * K + 32 * b + i] = (int8_t)q;
             }
@@ -198,32 +203,37 @@ void or_gemm_q8(int kind, const uint8_t* W, const int8_t* xq, const float* xd, i
     const size_t rb = or_q8_row_bytes(kind, K);
     const int nblk = K / 32;
     const int has_min = kind == KQ2 || kind == KQ4 || kind == KQ5;
-    int32_t q[32];
-    float ws[2], wm[2];
+    /* the row's blocks decoded once: q [nblk][32], ws/wm [nblk][2] */
+    int32_t* q = (int32_t*)malloc(sizeof(int32_t) * (size_t)K);
+    float* ws = (float*)malloc(sizeof(float) * 2 * (size_t)nblk);
+    float* wm = (float*)malloc(sizeof(float) * 2 * (size_t)nblk);
     for (int n = 0; n < N; ++n) {
         const uint8_t* row = W + (size_t)n * rb;
+        for (int b = 0; b < nblk; ++b) or_kq_block(kind, row, b, q + 32 * b, ws + 2 * b, wm + 2 * b);
         for (int t = 0; t < T; ++t) {
             const int8_t* x = xq + (size_t)t * K;
             float acc = 0.0f;
             for (int b = 0; b < nblk; ++b) {
-                or_kq_block(kind, row, b, q, ws, wm);
                 int dot[2] = {0, 0}, bsum[2] = {0, 0};
                 for (int l = 0; l < 32; ++l) {
-                    dot[l >> 4] += q[l] * x[32 * b + l];
+                    dot[l >> 4] += q[32 * b + l] * x[32 * b + l];
                     bsum[l >> 4] += x[32 * b + l];
                 }
                 const float dx = xd[(size_t)t * nblk + b];
                 /* integer value of the block against its scales: one fp32 product
                  * per 16 values (both halves share ws for the per-32 kinds) */
-                acc = fmaf(dx * ws[0], (float)dot[0], acc);
-                acc = fmaf(dx * ws[1], (float)dot[1], acc);
+                acc = fmaf(dx * ws[2 * b], (float)dot[0], acc);
+                acc = fmaf(dx * ws[2 * b + 1], (float)dot[1], acc);
                 if (has_min) {
-                    acc = fmaf(-wm[0], dx * (float)bsum[0], acc);
-                    acc = fmaf(-wm[1], dx * (float)bsum[1], acc);
+                    acc = fmaf(-wm[2 * b], dx * (float)bsum[0], acc);
+                    acc = fmaf(-wm[2 * b + 1], dx * (float)bsum[1], acc);
                 }
             }
             if (yraw) yraw[(size_t)t * N + n] = acc;
             if (Y) Y[(size_t)t * ldy + n] = store_y(acc, bias, res ? res + (size_t)t * ldy : NULL, n);
         }
     }
+    free(q);
+    free(ws);
+    free(wm);
 }

@@ -18,7 +18,7 @@ FAKE = 0x1000  # non-null pointer value: every call below must fail before touch
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(friday_attn_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(friday_(?:attn|gemm|quantize|q8)_\w+)\s*\(", text)))
 
 
 def test_header_and_binding_agree(fa):
@@ -144,3 +144,27 @@ def test_cpp_shim_compiles():
         r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
                             "-I", "/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", f], capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
+
+
+def test_gemm_q8_validation(fa):
+    """gemmQ8Supported rules (prefill_kernels.cu:340: a known kind and K % 256 == 0) and the
+    argument checks that run before any HIP call."""
+    L = fa.load()
+    assert L.friday_gemm_q8_supported(fa.Q4_K, 4096) == 1 and L.friday_gemm_q8_supported(fa.Q8_0, 256) == 1
+    assert L.friday_gemm_q8_supported(fa.Q4_K, 4000) == 0 and L.friday_gemm_q8_supported(0, 4096) == 0
+    assert L.friday_gemm_q8_supported(7, 4096) == 0
+    # unsupported kind / K (the reference aborts there, prefill_kernels.cu:344-347)
+    assert L.friday_gemm_q8(fa.Q4_K, FAKE, FAKE, FAKE, 4, 1000, 64, FAKE, 64, None, None, None) == fa.FA_ERR_UNSUPPORTED
+    assert "K" in err(fa)
+    # T <= 0: nothing to do
+    assert L.friday_gemm_q8(fa.Q4_K, FAKE, FAKE, FAKE, 0, 256, 64, FAKE, 64, None, None, None) == fa.FA_OK
+    # ldy < N, null Y, misaligned xq
+    assert L.friday_gemm_q8(fa.Q4_K, FAKE, FAKE, FAKE, 4, 256, 64, FAKE, 32, None, None, None) == fa.FA_ERR_INVALID
+    assert L.friday_gemm_q8(fa.Q4_K, FAKE, FAKE, FAKE, 4, 256, 64, None, 64, None, None, None) == fa.FA_ERR_INVALID
+    assert L.friday_gemm_q8(fa.Q4_K, FAKE, FAKE + 4, FAKE, 4, 256, 64, FAKE, 64, None, None, None) == fa.FA_ERR_INVALID
+    # row bytes of the GGML layouts
+    assert [L.friday_q8_row_bytes(k, 512) for k in range(1, 7)] == [168, 220, 288, 352, 420, 544]
+    assert L.friday_q8_row_bytes(fa.Q2_K, 300) == 0
+    # activation quantiser: K multiple of 32
+    assert L.friday_quantize_q8_rows(FAKE, 2, 48, FAKE, FAKE, None) == fa.FA_ERR_INVALID
+    assert L.friday_quantize_q8_rows(FAKE, 0, 64, FAKE, FAKE, None) == fa.FA_OK

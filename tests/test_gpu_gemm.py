@@ -1,0 +1,99 @@
+"""GPU parity of the prefill projection GEMM (friday_gemm_q8) and the activation
+quantiser (friday_quantize_q8_rows) against the CPU oracle.
+
+Mirrors tests/kernels/test_prefill_gemm.cu: every weight kind at its three shapes
+(T, K, N) = (1, 512, 64), (37, 1024, 200), (130, 768, 96) with bias + in-place residual,
+random blocks with fp16 scales in [1e-3, 1e-2], x and res N(0,1), bias 0.1 N(0,1); the bar is
+that test's (rel-L2 < 1e-3, max |diff| < 1e-2 of the RMS). The quantiser is bit-exact.
+Adds a 32B-model projection shape on sampled rows and ldy > N with untouched padding.
+"""
+import numpy as np
+import pytest
+
+from fa_helpers import KQ_KINDS, assert_gemm_close, kq_random_weights
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 512, 64, False), (37, 1024, 200, False), (130, 768, 96, True)]
+
+
+def run_gemm(fa, kind, W, x, T, K, N, bias=None, res=None, ldy=None, y_init=None):
+    ldy = N if ldy is None else ldy
+    dW = fa.DeviceBuffer.from_array(W)
+    dx = fa.DeviceBuffer.from_array(x)
+    dq = fa.DeviceBuffer(T * K)
+    dd = fa.DeviceBuffer(T * (K // 32) * 4)
+    fa.quantizeQ8Rows(dx, T, K, dq, dd)
+    Y0 = np.zeros((T, ldy), np.uint16) if y_init is None else y_init
+    dY = fa.DeviceBuffer.from_array(np.ascontiguousarray(Y0))
+    db = fa.DeviceBuffer.from_array(bias) if bias is not None else None
+    # residual in place, as the engine uses it: res and Y are the same buffer
+    fa.gemmQ8(kind, dW, dq, dd, T, K, N, dY, ldy, bias=db, res=dY if res else None)
+    fa.Hip.sync()
+    return (dY.download((T, ldy), np.uint16), dq.download((T, K), np.int8),
+            dd.download((T, K // 32), np.float32))
+
+
+@pytest.mark.parametrize("T,K,N,epi", SHAPES)
+@pytest.mark.parametrize("kind", sorted(KQ_KINDS))
+def test_reference_gemm_cases(gpu, oracle, kind, T, K, N, epi):
+    fa = gpu
+    rng = np.random.default_rng(20261110 + 10 * kind + T)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    res = rng.standard_normal((T, N), dtype=np.float32).astype(np.float16).view(np.uint16)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32) if epi else None
+    Y, xq, xd = run_gemm(fa, kind, W, x, T, K, N, bias=bias, res=epi, y_init=res if epi else None)
+    oq, od = oracle.quantize_q8_rows(x)
+    assert np.array_equal(xq, oq) and np.array_equal(xd.view(np.uint32), od.view(np.uint32))
+    ref, _ = oracle.gemm_q8(kind, W, oq, od, T, K, N, bias=bias, res=res if epi else None)
+    got = Y.view(np.float16).astype(np.float32)
+    assert_gemm_close(got, ref.view(np.float16).astype(np.float32), f"{KQ_KINDS[kind][0]} T={T} K={K} N={N}")
+
+
+def test_quantize_rows_edge_values(gpu, oracle):
+    fa = gpu
+    rng = np.random.default_rng(3)
+    rows, K = 9, 1024
+    x = (rng.standard_normal((rows, K), dtype=np.float32) * 5).astype(np.float16)
+    x[0, :32] = 0                         # zero block: d = 0, q = 0
+    x[1, 40] = np.float16(65504.0)        # fp16 max dominates its block
+    x[2, 64:96] = np.float16(6e-8)        # subnormal block
+    x[3, 100] = np.float16(-np.inf)       # amax = inf: d = inf, inv = 0
+    dx = fa.DeviceBuffer.from_array(x.view(np.uint16))
+    dq, dd = fa.DeviceBuffer(rows * K), fa.DeviceBuffer(rows * K // 32 * 4)
+    fa.quantizeQ8Rows(dx, rows, K, dq, dd)
+    fa.Hip.sync()
+    oq, od = oracle.quantize_q8_rows(x.view(np.uint16))
+    assert np.array_equal(dq.download((rows, K), np.int8), oq)
+    assert np.array_equal(dd.download((rows, K // 32), np.float32).view(np.uint32), od.view(np.uint32))
+
+
+def test_ldy_padding_untouched(gpu, oracle):
+    fa = gpu
+    kind, T, K, N, ldy = 3, 20, 512, 70, 96
+    rng = np.random.default_rng(11)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    canary = np.full((T, ldy), 0x7BCD, np.uint16)
+    Y, xq, xd = run_gemm(fa, kind, W, x, T, K, N, ldy=ldy, y_init=canary)
+    assert (Y[:, N:] == 0x7BCD).all()
+    ref, _ = oracle.gemm_q8(kind, W, xq, xd, T, K, N)
+    assert_gemm_close(Y[:, :N].view(np.float16).astype(np.float32), ref.view(np.float16).astype(np.float32), "ldy")
+
+
+@pytest.mark.parametrize("kind,K,N", [(1, 5120, 27648), (2, 27648, 5120), (3, 4096, 14336), (5, 14336, 4096)])
+def test_model_projection_shapes(gpu, oracle, kind, K, N):
+    """The reference's GEMM bench shapes (test_prefill_gemm.cu:40-42), T = 512; the oracle
+    checks 48 sampled weight rows (every token), the rest only for finiteness."""
+    fa = gpu
+    T = 512
+    rng = np.random.default_rng(kind + K)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    Y, xq, xd = run_gemm(fa, kind, W, x, T, K, N)
+    got = Y.view(np.float16).astype(np.float32)
+    assert np.isfinite(got).all()
+    rows = np.unique(np.concatenate([[0, 1, 127, 128, N - 1], rng.choice(N, 43, replace=False)]))
+    ref, _ = oracle.gemm_q8(kind, np.ascontiguousarray(W[rows]), xq, xd, T, K, len(rows))
+    assert_gemm_close(got[:, rows], ref.view(np.float16).astype(np.float32), f"{KQ_KINDS[kind][0]} K={K} N={N}")
