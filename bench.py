@@ -287,6 +287,42 @@ def prefill_config(cx, p0, steps, warmup):
             "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "tokens_per_s": round(T / (ms * 1e-3), 0)}
 
 
+# The reference's GEMM bench shapes (test_prefill_gemm.cu:40-42): kind code, K, N, what
+GEMM_CASES = [(3, 4096, 14336, "8B ffn_gate Q4_K"), (5, 14336, 4096, "8B ffn_down Q6_K"),
+              (1, 5120, 27648, "32B ffn_gate Q2_K"), (2, 27648, 5120, "32B ffn_down Q3_K")]
+KQ_LAYOUT = {1: (84, 256, (80, 82)), 2: (110, 256, (108,)), 3: (144, 256, (0, 2)), 4: (176, 256, (0, 2)),
+             5: (210, 256, (208,)), 6: (34, 32, (0,))}
+
+
+def gemm_config(cx, kind, K, N, what, steps, warmup):
+    """Prefill projection GEMM (friday_gemm_q8) at T = 512: random K-quant blocks with fp16
+    scales in [1e-3, 1e-2], random int8 activations; fp16 MFMA utilisation and weight bytes."""
+    import numpy as np
+
+    fa = cx.fa
+    T = 512
+    bb, vals, offs = KQ_LAYOUT[kind]
+    rng = np.random.default_rng(kind)
+    W = rng.integers(0, 256, size=(N, K // vals, bb), dtype=np.uint8)
+    for off in offs:
+        W[:, :, off:off + 2] = rng.uniform(1e-3, 1e-2, size=(N, K // vals)).astype(np.float16).view(
+            np.uint8).reshape(N, K // vals, 2)
+    dW = fa.DeviceBuffer.from_array(W.reshape(N, -1))
+    wbytes = W.nbytes
+    del W
+    xq, xd = fa.DeviceBuffer(T * K), fa.DeviceBuffer.from_array(np.full((T, K // 32), 0.01, np.float32))
+    cx.fill(xq, T * K // 2, 13)
+    Y = fa.DeviceBuffer(T * N * 2)
+    ms = cx.timed(lambda: fa.gemmQ8(kind, dW, xq, xd, T, K, N, Y, N, cx.stream.s), steps, warmup)
+    for b in (dW, xq, xd, Y):
+        b.free()
+    flops = 2.0 * T * K * N
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"config": "prefill projection GEMM", "what": what, "T": T, "K": K, "N": N, "us": round(ms * 1e3, 1),
+            "tflops": round(tf, 1), "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+            "weight_MB": round(wbytes / 1e6, 1)}
+
+
 def q8_config(cx, S, L, steps, warmup):
     """int8 KV (FRIDAY --kv q8) at the headline shape: one friday_attn_decode_step_q8 per layer."""
     import numpy as np
@@ -380,7 +416,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other BASELINE configs")
     args = ap.parse_args()
 
@@ -404,6 +440,8 @@ def main():
             lines.append(prefill_config(cx, p0, args.steps, args.warmup))
         lines.append(paged_config(cx, args.steps, args.warmup))
         lines.append(q8_config(cx, 32768, 64, args.steps, args.warmup))
+        for case in GEMM_CASES:
+            lines.append(gemm_config(cx, *case, args.steps, args.warmup))
         for rec in lines:
             print(json.dumps(rec), flush=True)
     if args.config == "q8":
@@ -413,6 +451,9 @@ def main():
     if args.config == "prefill":
         for p0 in (0, 1024, 2048, 4096, 7680):
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup)), flush=True)
+    if args.config == "gemm":
+        for case in GEMM_CASES:
+            print(json.dumps(gemm_config(cx, *case, args.steps, args.warmup)), flush=True)
 
 
 if __name__ == "__main__":

@@ -5,15 +5,17 @@
 // tensor cores and scales each in fp32 (prefill_kernels.cu:173-327); on CDNA that
 // per-block scaling is vector work six times the matrix work, so here both operands are
 // decoded once per workgroup into fp16 tiles in LDS (each value rounded once from its
-// exact fp32 form) and a single fp16 MFMA chain with fp32 accumulation runs over K.
+// exact fp32 form; activations as q times their scale rounded to fp16) and a single fp16
+// MFMA chain with fp32 accumulation runs over K.
 //
 // Tiling: a workgroup of 256 threads owns 128 weight rows x 128 tokens; its four waves
 // each own 64 x 64 (2 x 2 tiles of v_mfma_f32_32x32x16_f16). K advances in stages of 64
 // values through two LDS buffers: while the MFMAs consume one, the raw bytes of the next
-// stage are in flight in registers, then decoded into the other buffer.
+// stage are decoded into the other and those of the stage after it are in flight.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
@@ -21,10 +23,7 @@
 namespace fa {
 namespace {
 
-constexpr int kGBN = 128;  // weight rows per workgroup
-constexpr int kGBT = 128;  // tokens per workgroup
-constexpr int kGBK = 64;   // K values per stage (two 32-value blocks)
-constexpr int kGThreads = 256;
+constexpr int kGBK = 64;  // K values per stage (two 32-value blocks)
 constexpr int kGRowB = kGBK * 2;  // bytes of one fp16 tile row in LDS
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
@@ -51,8 +50,10 @@ struct WBlock {
 
 // get_scale_min_k4: 6-bit scale and min of block j (0..7) of a Q4_K / Q5_K superblock
 __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc, int& m) {
-    const uint32_t s[3] = {s0, s1, s2};
-    auto byte = [&](int i) { return (int)((s[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+    auto byte = [&](int i) {
+        const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+        return (int)((w >> (8 * (i & 3))) & 0xFF);
+    };
     if (j < 4) {
         sc = byte(j) & 63;
         m = byte(j + 4) & 63;
@@ -62,25 +63,84 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
     }
 }
 
-// Raw loads and decode of block `blk` (0..K/32-1) of one weight row, per GGML layout:
+// Raw words of block `blk` (0..K/32-1) of one weight row, per GGML layout:
 //   Q2_K  scales[16] qs[64] d dmin              84 B / 256, q = 2 bits, per-16 4-bit scale & min
 //   Q3_K  hmask[32] qs[64] scales[12] d         110 B, q = 2 bits + hmask bit - 4, per-16 6-bit scale - 32
 //   Q4_K  d dmin scales[12] qs[128]             144 B, q = nibble, per-32 6-bit scale & min
 //   Q5_K  d dmin scales[12] qh[32] qs[128]      176 B, q = nibble + qh bit << 4
 //   Q6_K  ql[128] qh[64] scales[16] d           210 B, q = nibble + 2 bits << 4 - 32, per-16 int8 scale
 //   Q8_0  d qs[32]                              34 B / 32, q = int8
-// (dequant32, prefill_kernels.cu:57-144; dequantizeRow, cpu_kquants.cpp:227-280)
+// (dequant32, prefill_kernels.cu:57-144; dequantizeRow, cpu_kquants.cpp:227-280).
+// load_wraw only issues the loads; decode_wraw does the bit work once they are needed, so
+// the loads of the next stage stay in flight across this stage's MFMAs.
+struct WRaw {
+    uint32_t a[8], b[8];  // the block's quant bits (qs / ql) and high bits (hmask / qh)
+    uint32_t s[3];        // packed scales
+    uint32_t d;           // fp16 d (and dmin)
+};
+
 template <int KIND>
-__device__ __forceinline__ void load_wblock(const uint8_t* row, int blk, WBlock& o) {
+__device__ __forceinline__ void load_wraw(const uint8_t* row, int blk, WRaw& r) {
     const int sb = blk >> 3, j = blk & 7;
     if constexpr (KIND == kKqQ2K) {
         const uint8_t* b = row + (size_t)sb * 84;
         const int h = j >> 2, s = j & 3;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) o.u[w] = (ld32(b + 16 + 32 * h + 4 * w) >> (2 * s)) & 0x03030303u;
-        const uint32_t scw = ld32(b + 8 * h + 4 * (s >> 1)) >> (16 * (s & 1));
-        const uint32_t dd = ld32(b + 80);
-        const float d = half_bits(dd & 0xFFFF), dmin = half_bits(dd >> 16);
+        for (int w = 0; w < 8; ++w) r.a[w] = ld32(b + 16 + 32 * h + 4 * w);
+        r.s[0] = ld32(b + 8 * h + 4 * (s >> 1));
+        r.d = ld32(b + 80);
+    } else if constexpr (KIND == kKqQ3K) {
+        const uint8_t* b = row + (size_t)sb * 110;
+        const int h = j >> 2;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            r.a[w] = ld16x2(b + 32 + 32 * h + 4 * w);
+            r.b[w] = ld16x2(b + 4 * w);
+        }
+        r.s[0] = ld16x2(b + 96);
+        r.s[1] = ld16x2(b + 100);
+        r.s[2] = ld16x2(b + 104);
+        r.d = ld16(b + 108);
+    } else if constexpr (KIND == kKqQ4K || KIND == kKqQ5K) {
+        constexpr bool Q5 = KIND == kKqQ5K;
+        const uint8_t* b = row + (size_t)sb * (Q5 ? 176 : 144);
+        const uint8_t* qs = b + (Q5 ? 48 : 16) + 32 * (j >> 1);
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            r.a[w] = ld32(qs + 4 * w);
+            if constexpr (Q5) r.b[w] = ld32(b + 16 + 4 * w);
+        }
+        r.s[0] = ld32(b + 4);
+        r.s[1] = ld32(b + 8);
+        r.s[2] = ld32(b + 12);
+        r.d = ld32(b);
+    } else if constexpr (KIND == kKqQ6K) {
+        const uint8_t* b = row + (size_t)sb * 210;
+        const int h = j >> 2, p = j & 3;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            r.a[w] = ld16x2(b + 64 * h + 32 * (p & 1) + 4 * w);
+            r.b[w] = ld16x2(b + 128 + 32 * h + 4 * w);
+        }
+        r.s[0] = ld16(b + 192 + 8 * h + 2 * p);
+        r.d = ld16(b + 208);
+    } else {  // Q8_0
+        const uint8_t* b = row + (size_t)blk * 34;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) r.a[w] = ld16x2(b + 2 + 4 * w);
+        r.d = ld16(b);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void decode_wraw(const WRaw& r, int blk, WBlock& o) {
+    const int j = blk & 7;
+    if constexpr (KIND == kKqQ2K) {
+        const int s = j & 3;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) o.u[w] = (r.a[w] >> (2 * s)) & 0x03030303u;
+        const uint32_t scw = r.s[0] >> (16 * (s & 1));
+        const float d = half_bits(r.d & 0xFFFF), dmin = half_bits(r.d >> 16);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int sc = (scw >> (8 * c)) & 0xFF;
@@ -88,18 +148,18 @@ __device__ __forceinline__ void load_wblock(const uint8_t* row, int blk, WBlock&
             o.c[c] = -(dmin * (float)(sc >> 4));
         }
     } else if constexpr (KIND == kKqQ3K) {
-        const uint8_t* b = row + (size_t)sb * 110;
         const int h = j >> 2, s = j & 3;
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-            const uint32_t lo = (ld16x2(b + 32 + 32 * h + 4 * w) >> (2 * s)) & 0x03030303u;
-            const uint32_t hb = (ld16x2(b + 4 * w) >> (4 * h + s)) & 0x01010101u;
+            const uint32_t lo = (r.a[w] >> (2 * s)) & 0x03030303u;
+            const uint32_t hb = (r.b[w] >> (4 * h + s)) & 0x01010101u;
             o.u[w] = lo | (hb << 2);  // q + 4, 0..7
         }
-        const uint32_t s0 = ld16x2(b + 96), s1 = ld16x2(b + 100), s2 = ld16x2(b + 104);
-        const uint32_t sw[3] = {s0, s1, s2};
-        auto byte = [&](int i) { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xFF); };
-        const float d = half_bits(ld16(b + 108));
+        auto byte = [&](int i) {  // selects, not an indexed array (which would live in scratch)
+            const uint32_t w = i < 4 ? r.s[0] : (i < 8 ? r.s[1] : r.s[2]);
+            return (int)((w >> (8 * (i & 3))) & 0xFF);
+        };
+        const float d = half_bits(r.d);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int g = 8 * h + 2 * s + c;
@@ -109,43 +169,35 @@ __device__ __forceinline__ void load_wblock(const uint8_t* row, int blk, WBlock&
             o.c[c] = -4.0f * o.ws[c];
         }
     } else if constexpr (KIND == kKqQ4K || KIND == kKqQ5K) {
-        constexpr bool Q5 = KIND == kKqQ5K;
-        const uint8_t* b = row + (size_t)sb * (Q5 ? 176 : 144);
-        const int jj = j >> 1, hi = j & 1;
-        const uint8_t* qs = b + (Q5 ? 48 : 16) + 32 * jj;
+        const int hi = j & 1;
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-            uint32_t v = (ld32(qs + 4 * w) >> (4 * hi)) & 0x0F0F0F0Fu;
-            if constexpr (Q5) v |= ((ld32(b + 16 + 4 * w) >> j) & 0x01010101u) << 4;
+            uint32_t v = (r.a[w] >> (4 * hi)) & 0x0F0F0F0Fu;
+            if constexpr (KIND == kKqQ5K) v |= ((r.b[w] >> j) & 0x01010101u) << 4;
             o.u[w] = v;
         }
         int sc, m;
-        scale_min_k4(j, ld32(b + 4), ld32(b + 8), ld32(b + 12), sc, m);
-        const uint32_t dd = ld32(b);
-        o.ws[0] = o.ws[1] = half_bits(dd & 0xFFFF) * (float)sc;
-        o.c[0] = o.c[1] = -(half_bits(dd >> 16) * (float)m);
+        scale_min_k4(j, r.s[0], r.s[1], r.s[2], sc, m);
+        o.ws[0] = o.ws[1] = half_bits(r.d & 0xFFFF) * (float)sc;
+        o.c[0] = o.c[1] = -(half_bits(r.d >> 16) * (float)m);
     } else if constexpr (KIND == kKqQ6K) {
-        const uint8_t* b = row + (size_t)sb * 210;
-        const int h = j >> 2, p = j & 3;
+        const int p = j & 3;
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-            const uint32_t ql = ld16x2(b + 64 * h + 32 * (p & 1) + 4 * w);
-            const uint32_t lo = (p < 2 ? ql : ql >> 4) & 0x0F0F0F0Fu;
-            const uint32_t hb = (ld16x2(b + 128 + 32 * h + 4 * w) >> (2 * p)) & 0x03030303u;
+            const uint32_t lo = (p < 2 ? r.a[w] : r.a[w] >> 4) & 0x0F0F0F0Fu;
+            const uint32_t hb = (r.b[w] >> (2 * p)) & 0x03030303u;
             o.u[w] = lo | (hb << 4);  // q + 32, 0..63
         }
-        const uint32_t scp = ld16(b + 192 + 8 * h + 2 * p);
-        const float d = half_bits(ld16(b + 208));
+        const float d = half_bits(r.d);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            o.ws[c] = d * (float)(int8_t)((scp >> (8 * c)) & 0xFF);
+            o.ws[c] = d * (float)(int8_t)((r.s[0] >> (8 * c)) & 0xFF);
             o.c[c] = -32.0f * o.ws[c];
         }
     } else {  // Q8_0
-        const uint8_t* b = row + (size_t)blk * 34;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) o.u[w] = ld16x2(b + 2 + 4 * w) ^ 0x80808080u;  // q + 128
-        o.ws[0] = o.ws[1] = half_bits(ld16(b));
+        for (int w = 0; w < 8; ++w) o.u[w] = r.a[w] ^ 0x80808080u;  // q + 128
+        o.ws[0] = o.ws[1] = half_bits(r.d);
         o.c[0] = o.c[1] = -128.0f * o.ws[0];
     }
 }
@@ -153,20 +205,66 @@ __device__ __forceinline__ void load_wblock(const uint8_t* row, int blk, WBlock&
 // byte i of w as a float (v_cvt_f32_ubyte{0..3})
 __device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xFF); }
 
-// 32 decoded values -> 64 bytes of row r of an fp16 tile at chunks 4*half .. 4*half+3,
-// each 16-byte chunk c stored at slot c ^ (r & 7) (conflict-free 16-byte MFMA operand reads)
-__device__ __forceinline__ void store_tile32(unsigned char* tile, int r, int half, const uint32_t (&u)[8],
-                                             const float (&ws)[2], const float (&c)[2]) {
+// LDS tiles: row r of a tile holds 64 fp16 values (128 bytes, eight 16-byte chunks); chunk c
+// is stored at slot c ^ ((r >> 1) & 7). A 16-byte access serves 16 lanes per cycle over a
+// 256-byte bank window (two rows): the 16 rows a fragment read touches then land on 16
+// distinct (row parity, slot) pairs, and so do the 8 rows x 2 halves of a tile write.
+__device__ __forceinline__ int tile_off(int r, int chunk) { return r * kGRowB + ((chunk ^ ((r >> 1) & 7)) * 16); }
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+// fp16(a * b + c) in one rounding, fp32 operands (v_fma_mix), into the low / high half of d
+__device__ __forceinline__ uint32_t fma_mix_lo(float a, float b, float c) {
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ uint32_t fma_mix_hi(uint32_t d, float a, float b, float c) {
+    asm("v_fma_mixhi_f16 %0, %1, %2, %3" : "+v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// 32 decoded weight values -> row r of an fp16 tile, chunks 4*half .. 4*half+3:
+// value l = fp16(ws[l/16] * byte_l + c[l/16]) rounded once from the exact fp32 form
+__device__ __forceinline__ void store_w32(unsigned char* tile, int r, int half, uint32_t (&u)[8],
+                                          const float (&ws)[2], const float (&c)[2]) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) asm volatile("" : "+v"(u[w]));  // keep the masked words: one cvt per byte
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) {
-        h8v v;
+        uint32_t o[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int l = 8 * ch + e;  // value index in the block
-            v[e] = (_Float16)__builtin_fmaf(ws[l >> 4], ubyte(u[l >> 2], l & 3), c[l >> 4]);
+        for (int e = 0; e < 4; ++e) {
+            const int l = 8 * ch + 2 * e;  // values l, l + 1 (bytes of word l / 4)
+            const uint32_t wd = u[l >> 2];
+            const float s = ws[l >> 4], cc = c[l >> 4];
+            const float b0 = ubyte(wd, l & 3), b1 = ubyte(wd, (l & 3) + 1);
+            o[e] = fma_mix_hi(fma_mix_lo(s, b0, cc), s, b1, cc);
         }
-        const int slot = (4 * half + ch) ^ (r & 7);
-        *reinterpret_cast<h8v*>(tile + r * kGRowB + slot * 16) = v;
+        *reinterpret_cast<uint4*>(tile + tile_off(r, 4 * half + ch)) = uint4{o[0], o[1], o[2], o[3]};
+    }
+}
+
+// 32 int8 activations (two 16-byte words) and their fp32 scale -> row r of an fp16 tile:
+// byte (q ^ 0x80) spliced under the fp16 exponent byte 0x66 is 1664 + q exactly; minus 1664
+// (exact) times the scale rounded to fp16, in packed fp16 (one rounding of q * fp16(xd))
+__device__ __forceinline__ void store_x32(unsigned char* tile, int r, int half, const uint4& xa, const uint4& xb,
+                                          float xd) {
+    const h2v s2 = h2v{(_Float16)xd, (_Float16)xd};
+    const h2v bias = h2v{(_Float16)1664.0f, (_Float16)1664.0f};
+    const uint32_t in[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t u = in[2 * ch + i] ^ 0x80808080u;
+            const uint32_t d0 = __builtin_amdgcn_perm(0x66666666u, u, 0x04010400u);  // bytes u0 66 u1 66
+            const uint32_t d1 = __builtin_amdgcn_perm(0x66666666u, u, 0x04030402u);  // bytes u2 66 u3 66
+            o[2 * i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2v, d0) - bias) * s2);
+            o[2 * i + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2v, d1) - bias) * s2);
+        }
+        *reinterpret_cast<uint4*>(tile + tile_off(r, 4 * half + ch)) = uint4{o[0], o[1], o[2], o[3]};
     }
 }
 
@@ -195,64 +293,81 @@ __device__ __forceinline__ uint16_t epilogue(float acc, const float* bias, const
     return h;
 }
 
-template <int KIND>
-__global__ __launch_bounds__(kGThreads, 2) void kq_gemm_kernel(KqGemmParams p) {
-    __shared__ __align__(16) unsigned char sw0[kGBN * kGRowB];
-    __shared__ __align__(16) unsigned char sw1[kGBN * kGRowB];
-    __shared__ __align__(16) unsigned char sx0[kGBT * kGRowB];
-    __shared__ __align__(16) unsigned char sx1[kGBT * kGRowB];
+// Workgroup shape: WVN x WVT waves, each owning TN x TT tiles of 32 x 32 (rows x tokens),
+// so BN = 32 WVN TN weight rows and BT = 32 WVT TT tokens per workgroup. Staging: thread
+// u < 2 BN decodes half u % 2 (32 values) of weight row u / 2 of each stage, thread
+// u >= NT - 2 BT the same for token row (u - (NT - 2 BT)) / 2.
+template <int KIND, int WVN, int WVT, int TN, int TT>
+__global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p) {
+    constexpr int NT = 64 * WVN * WVT;
+    constexpr int BN = 32 * WVN * TN, BT = 32 * WVT * TT;
+    static_assert(2 * BN <= NT && 2 * BT <= NT, "one staging unit per thread and role");
+    __shared__ __align__(16) unsigned char sw0[BN * kGRowB];
+    __shared__ __align__(16) unsigned char sw1[BN * kGRowB];
+    __shared__ __align__(16) unsigned char sx0[BT * kGRowB];
+    __shared__ __align__(16) unsigned char sx1[BT * kGRowB];
 
     // workgroup -> (row block, token block): the token blocks of one row block get ids
     // that are equal mod 8, so with round-robin placement over the 8 XCDs they share an
     // XCD and its L2 copy of the weight rows
-    const int nrb = (p.N + kGBN - 1) / kGBN, ntb = (p.T + kGBT - 1) / kGBT;
+    const int nrb = (p.N + BN - 1) / BN, ntb = (p.T + BT - 1) / BT;
     const int id = blockIdx.x;
     const int rb = (id % 8) + 8 * (id / (8 * ntb));
     const int tb = (id / 8) % ntb;
     if (rb >= nrb) return;  // padding of the last group of 8 row blocks
-    const int n0 = rb * kGBN, t0 = tb * kGBT;
+    const int n0 = rb * BN, t0 = tb * BT;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1, wt = wave >> 1;
+    const int wn = wave % WVN, wt = wave / WVN;
 
-    // staging role: weight row n0 + lr, block half lh of the stage; token t0 + lr, half lh
-    const int lr = tid >> 1, lh = tid & 1;
+    // staging roles (wave-uniform: 2 BN and NT - 2 BT are multiples of 64)
+    const bool w_role = tid < 2 * BN;
+    const bool x_role = tid >= NT - 2 * BT;
+    const int wr_ = tid >> 1, xr_ = (tid - (NT - 2 * BT)) >> 1, lh = tid & 1;
     const size_t row_bytes = p.row_bytes;
-    const bool w_ok = n0 + lr < p.N;
-    const bool x_ok = t0 + lr < p.T;
-    const uint8_t* wrow = p.W + (size_t)(w_ok ? n0 + lr : 0) * row_bytes;
-    const int8_t* xrow = p.xq + (size_t)(x_ok ? t0 + lr : 0) * p.K;
-    const float* xdrow = p.xd + (size_t)(x_ok ? t0 + lr : 0) * (p.K / 32);
+    const bool w_ok = w_role && n0 + wr_ < p.N;
+    const bool x_ok = x_role && t0 + xr_ < p.T;
+    const uint8_t* wrow = p.W + (size_t)(w_ok ? n0 + wr_ : 0) * row_bytes;
+    const int8_t* xrow = p.xq + (size_t)(x_ok ? t0 + xr_ : 0) * p.K;
+    const float* xdrow = p.xd + (size_t)(x_ok ? t0 + xr_ : 0) * (p.K / 32);
+    const bool w_wave = __builtin_amdgcn_readfirstlane(w_role);
+    const bool x_wave = __builtin_amdgcn_readfirstlane(x_role);
 
-    WBlock wb;
-    uint4 xa, xb;
-    float xs;
-    auto load_stage = [&](int k0) __attribute__((always_inline)) {
-        const int blk = k0 / 32 + lh;
-        load_wblock<KIND>(wrow, blk, wb);
-        xa = *reinterpret_cast<const uint4*>(xrow + 32 * blk);
-        xb = *reinterpret_cast<const uint4*>(xrow + 32 * blk + 16);
-        xs = xdrow[blk];
+    // raw operands of one stage in registers; two sets, so that the loads of stage s + 2
+    // are in flight across the MFMAs of stage s and the decode of stage s + 1
+    struct Raw {
+        WRaw w;
+        uint4 xa, xb;
+        float xs;
     };
-    auto store_stage = [&](unsigned char* sw, unsigned char* sx) __attribute__((always_inline)) {
-        if (!w_ok) {
-            wb.ws[0] = wb.ws[1] = wb.c[0] = wb.c[1] = 0.0f;
+    Raw raw0, raw1;
+    auto load_stage = [&](Raw& r, int st) __attribute__((always_inline)) {
+        const int blk = st * (kGBK / 32) + lh;
+        if (w_wave) load_wraw<KIND>(wrow, blk, r.w);
+        if (x_wave) {
+            r.xa = *reinterpret_cast<const uint4*>(xrow + 32 * blk);
+            r.xb = *reinterpret_cast<const uint4*>(xrow + 32 * blk + 16);
+            r.xs = xdrow[blk];
         }
-        store_tile32(sw, lr, lh, wb.u, wb.ws, wb.c);
-        // activations: q = byte ^ 0x80 - 128, value = fp16(xd * q) from fma(xd, q + 128, -128 xd)
-        const uint32_t xu[8] = {xa.x ^ 0x80808080u, xa.y ^ 0x80808080u, xa.z ^ 0x80808080u, xa.w ^ 0x80808080u,
-                                xb.x ^ 0x80808080u, xb.y ^ 0x80808080u, xb.z ^ 0x80808080u, xb.w ^ 0x80808080u};
-        const float s = x_ok ? xs : 0.0f;
-        const float xsv[2] = {s, s}, xc[2] = {-128.0f * s, -128.0f * s};
-        store_tile32(sx, lr, lh, xu, xsv, xc);
+    };
+    auto store_stage = [&](const Raw& r, int st, unsigned char* sw, unsigned char* sx) __attribute__((always_inline)) {
+        if (w_wave) {
+            WBlock wb;
+            decode_wraw<KIND>(r.w, st * (kGBK / 32) + lh, wb);
+            if (!w_ok) {
+                wb.ws[0] = wb.ws[1] = wb.c[0] = wb.c[1] = 0.0f;
+            }
+            store_w32(sw, wr_, lh, wb.u, wb.ws, wb.c);
+        }
+        if (x_wave) store_x32(sx, xr_, lh, r.xa, r.xb, x_ok ? r.xs : 0.0f);
     };
 
-    f16v acc[2][2];
+    f16v acc[TN][TT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TT; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -260,54 +375,57 @@ __global__ __launch_bounds__(kGThreads, 2) void kq_gemm_kernel(KqGemmParams p) {
 #pragma unroll
         for (int kk = 0; kk < kGBK / 16; ++kk) {
             const int ch = 2 * kk + (lane >> 5);  // this lane's 8 K values of the 16
-            h8v a[2], b[2];
+            h8v a[TN], b[TT];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = wn * 64 + 32 * i + (lane & 31);
-                a[i] = *reinterpret_cast<const h8v*>(sw + r * kGRowB + ((ch ^ (r & 7)) * 16));
+            for (int i = 0; i < TN; ++i) {
+                const int r = (wn * TN + i) * 32 + (lane & 31);
+                a[i] = *reinterpret_cast<const h8v*>(sw + tile_off(r, ch));
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int r = wt * 64 + 32 * j + (lane & 31);
-                b[j] = *reinterpret_cast<const h8v*>(sx + r * kGRowB + ((ch ^ (r & 7)) * 16));
+            for (int j = 0; j < TT; ++j) {
+                const int r = (wt * TT + j) * 32 + (lane & 31);
+                b[j] = *reinterpret_cast<const h8v*>(sx + tile_off(r, ch));
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TN; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TT; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     };
 
+    // stage st: loads of st + 2 into the set that held st, MFMAs on LDS buffer st % 2,
+    // decode of st + 1 (loaded one stage earlier) into the other buffer, barrier
     const int nst = p.K / kGBK;
-    load_stage(0);
-    store_stage(sw0, sx0);
+    load_stage(raw0, 0);
+    if (nst > 1) load_stage(raw1, 1);
+    store_stage(raw0, 0, sw0, sx0);
     __syncthreads();
     for (int st = 0; st < nst; st += 2) {
-        if (st + 1 < nst) load_stage((st + 1) * kGBK);
+        if (st + 2 < nst) load_stage(raw0, st + 2);
         compute(sw0, sx0);
-        if (st + 1 < nst) store_stage(sw1, sx1);
+        if (st + 1 < nst) store_stage(raw1, st + 1, sw1, sx1);
         __syncthreads();
         if (st + 1 >= nst) break;
-        if (st + 2 < nst) load_stage((st + 2) * kGBK);
+        if (st + 3 < nst) load_stage(raw1, st + 3);
         compute(sw1, sx1);
-        if (st + 2 < nst) store_stage(sw0, sx0);
+        if (st + 2 < nst) store_stage(raw0, st + 2, sw0, sx0);
         __syncthreads();
     }
 
-    // acc[i][j][r]: weight row n0 + wn*64 + 32i + 8(r/4) + 4(lane/32) + r%4,
-    // token t0 + wt*64 + 32j + lane%32
+    // acc[i][j][r]: weight row n0 + (wn TN + i) 32 + 8(r/4) + 4(lane/32) + r%4,
+    // token t0 + (wt TT + j) 32 + lane%32
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int t = t0 + wt * 64 + 32 * j + (lane & 31);
+    for (int j = 0; j < TT; ++j) {
+        const int t = t0 + (wt * TT + j) * 32 + (lane & 31);
         if (t >= p.T) continue;
         uint16_t* yrow = p.Y + (size_t)t * p.ldy;
         const uint16_t* rrow = p.res ? p.res + (size_t)t * p.ldy : nullptr;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int n = n0 + wn * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int n = n0 + (wn * TN + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (n < p.N) yrow[n] = epilogue(acc[i][j][r], p.bias, rrow, n);
             }
     }
@@ -333,21 +451,41 @@ __global__ __launch_bounds__(256) void quantize_q8_rows_kernel(const uint16_t* _
     if ((idx & 31) == 0) xd[row * (K / 32) + blk] = d;
 }
 
-}  // namespace
-
-int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
-    const int nrb = (p.N + kGBN - 1) / kGBN, ntb = (p.T + kGBT - 1) / kGBT;
-    const dim3 grid(((nrb + 7) / 8) * 8 * ntb);
+template <int WVN, int WVT, int TN, int TT>
+int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
+    constexpr int BN = 32 * WVN * TN, BT = 32 * WVT * TT;
+    const int nrb = (p.N + BN - 1) / BN, ntb = (p.T + BT - 1) / BT;
+    const dim3 grid(((nrb + 7) / 8) * 8 * ntb), block(64 * WVN * WVT);
     switch (kind) {
-        case kKqQ2K: hipLaunchKernelGGL(kq_gemm_kernel<kKqQ2K>, grid, dim3(kGThreads), 0, stream, p); break;
-        case kKqQ3K: hipLaunchKernelGGL(kq_gemm_kernel<kKqQ3K>, grid, dim3(kGThreads), 0, stream, p); break;
-        case kKqQ4K: hipLaunchKernelGGL(kq_gemm_kernel<kKqQ4K>, grid, dim3(kGThreads), 0, stream, p); break;
-        case kKqQ5K: hipLaunchKernelGGL(kq_gemm_kernel<kKqQ5K>, grid, dim3(kGThreads), 0, stream, p); break;
-        case kKqQ6K: hipLaunchKernelGGL(kq_gemm_kernel<kKqQ6K>, grid, dim3(kGThreads), 0, stream, p); break;
-        case kKqQ80: hipLaunchKernelGGL(kq_gemm_kernel<kKqQ80>, grid, dim3(kGThreads), 0, stream, p); break;
+        case kKqQ2K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ2K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
+        case kKqQ3K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ3K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
+        case kKqQ4K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ4K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
+        case kKqQ5K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ5K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
+        case kKqQ6K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ6K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
+        case kKqQ80: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ80, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+// Tile shape: 256 x 128 (eight waves, one workgroup per CU) when that alone fills the 256
+// CUs, else 128 x 128 (four waves, two per CU) when it gives at least 1.5 workgroups per
+// CU, else 64 x 64 (four waves, one tile each) so that small-N / large-K shapes still
+// spread over the chip. FRIDAY_GEMM_TILE = 1 / 2 / 3 forces one of them.
+int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
+    static const int forced = [] {
+        const char* e = std::getenv("FRIDAY_GEMM_TILE");
+        return e && *e ? std::atoi(e) : 0;
+    }();
+    auto wgs = [&](int bn, int bt) { return (long)((p.N + bn - 1) / bn) * ((p.T + bt - 1) / bt); };
+    int shape = forced;
+    if (shape < 1 || shape > 4) shape = wgs(256, 128) >= 256 ? 1 : (wgs(128, 128) >= 384 ? 2 : 3);
+    if (shape == 1) return launch_kq_shape<4, 2, 2, 2>(kind, p, stream);
+    if (shape == 2) return launch_kq_shape<2, 2, 2, 2>(kind, p, stream);
+    if (shape == 4) return launch_kq_shape<2, 4, 2, 1>(kind, p, stream);
+    return launch_kq_shape<2, 2, 1, 1>(kind, p, stream);
 }
 
 int launch_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd, hipStream_t stream) {
