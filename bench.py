@@ -323,6 +323,44 @@ def gemm_config(cx, kind, K, N, what, steps, warmup):
             "weight_MB": round(wbytes / 1e6, 1)}
 
 
+# Decode GEMVs (friday_gemv_q8): the attention O-projection of Qwen2.5-32B (transformer.cpp:
+# 1057-1059) and the 8B ffn_down; kind code, K, N, what
+GEMV_CASES = [(3, 5120, 5120, "32B attn_output Q4_K"), (5, 14336, 4096, "8B ffn_down Q6_K")]
+
+
+def gemv_config(cx, kind, K, N, what, steps, warmup):
+    """One int8-activation GEMV per layer over layer-distinct weights (rotated beyond the MALL):
+    HBM bytes = the weight rows; us per layer and GB/s against the 8 TB/s peak."""
+    import numpy as np
+
+    fa = cx.fa
+    bb, vals, offs = KQ_LAYOUT[kind]
+    rng = np.random.default_rng(kind)
+    W = rng.integers(0, 256, size=(N, K // vals, bb), dtype=np.uint8)
+    for off in offs:
+        W[:, :, off:off + 2] = rng.uniform(1e-3, 1e-2, size=(N, K // vals)).astype(np.float16).view(
+            np.uint8).reshape(N, K // vals, 2)
+    W = W.reshape(N, -1)
+    wb = W.nbytes
+    L = max(2, -(-2 * MALL_BYTES // wb))
+    dW = fa.DeviceBuffer(L * wb)
+    for l in range(L):
+        dW.upload(W, l * wb)
+    del W
+    xq = fa.DeviceBuffer(K)
+    cx.fill(xq, K // 2, 17)
+    xd = fa.DeviceBuffer.from_array(np.full(K // 32, 0.01, np.float32))
+    y = fa.DeviceBuffer(N * 2)
+    ms = cx.timed(lambda: [fa.gemvQ8(kind, dW.ptr + l * wb, xq, xd, K, N, y, cx.stream.s) for l in range(L)],
+                  steps, warmup) / L
+    for b in (dW, xq, xd, y):
+        b.free()
+    gbs = wb / (ms * 1e-3) / 1e9
+    return {"config": "decode GEMV (int8 activations)", "what": what, "K": K, "N": N, "layers": L,
+            "us_per_layer": round(ms * 1e3, 2), "weight_MB": round(wb / 1e6, 2), "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def q8_config(cx, S, L, steps, warmup):
     """int8 KV (FRIDAY --kv q8) at the headline shape: one friday_attn_decode_step_q8 per layer."""
     import numpy as np
@@ -442,6 +480,8 @@ def main():
         lines.append(q8_config(cx, 32768, 64, args.steps, args.warmup))
         for case in GEMM_CASES:
             lines.append(gemm_config(cx, *case, args.steps, args.warmup))
+        for case in GEMV_CASES:
+            lines.append(gemv_config(cx, *case, args.steps, args.warmup))
         for rec in lines:
             print(json.dumps(rec), flush=True)
     if args.config == "q8":
@@ -454,6 +494,8 @@ def main():
     if args.config == "gemm":
         for case in GEMM_CASES:
             print(json.dumps(gemm_config(cx, *case, args.steps, args.warmup)), flush=True)
+        for case in GEMV_CASES:
+            print(json.dumps(gemv_config(cx, *case, args.steps, args.warmup)), flush=True)
 
 
 if __name__ == "__main__":

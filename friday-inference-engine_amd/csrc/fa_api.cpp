@@ -459,4 +459,24 @@ int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, i
     return launch_status(fa::launch_kq_gemm(kind, p, static_cast<hipStream_t>(stream)), w);
 }
 
+int friday_gemv_q8(int kind, const void* W, const int8_t* xq, const float* xd, int K, int N, uint16_t* y,
+                   void* stream, const void* W2, uint16_t* y2, const float* bias, const uint16_t* res) {
+    const char* w = "gemv_q8";
+    if (!kq_kind_ok(kind)) return fail(FA_ERR_UNSUPPORTED, "%s: unsupported type %d", w, kind);
+    if (K <= 0 || K % (kind == FA_KQ_Q8_0 ? 32 : 256))
+        return fail(FA_ERR_UNSUPPORTED, "%s: K=%d must be a multiple of %d", w, K, kind == FA_KQ_Q8_0 ? 32 : 256);
+    if (N <= 0) return fail(FA_ERR_INVALID, "%s: invalid N=%d", w, N);
+    if (!W || !xq || !xd || !y || (W2 && !y2)) return fail(FA_ERR_INVALID, "%s: null argument", w);
+    if (reinterpret_cast<uintptr_t>(W) % 4 || reinterpret_cast<uintptr_t>(W2) % 4 ||
+        reinterpret_cast<uintptr_t>(xq) % 16 || reinterpret_cast<uintptr_t>(xd) % 4)
+        return fail(FA_ERR_INVALID, "%s: misaligned W / W2 (4 B), xq (16 B) or xd", w);
+    if ((long long)N * (W2 ? 2 : 1) > 0x7fffffffLL - 3) return fail(FA_ERR_UNSUPPORTED, "%s: N too large", w);
+    fa::KqGemvParams p{};
+    p.W = static_cast<const uint8_t*>(W); p.W2 = static_cast<const uint8_t*>(W2); p.xq = xq; p.xd = xd;
+    p.y = y; p.y2 = y2; p.bias = bias; p.res = res;
+    p.row_bytes = friday_q8_row_bytes(kind, K);
+    p.K = K; p.N = N;
+    return launch_status(fa::launch_kq_gemv(kind, p, static_cast<hipStream_t>(stream)), w);
+}
+
 }  // extern "C"

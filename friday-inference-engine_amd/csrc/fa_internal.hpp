@@ -131,6 +131,19 @@ struct KqGemmParams {
     int T, K, N, ldy;
 };
 int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream);
+struct KqGemvParams {
+    const uint8_t* W;      // [N][row_bytes]
+    const uint8_t* W2;     // optional second matrix (rows N .. 2N - 1 of the launch), or null
+    const int8_t* xq;      // [K]
+    const float* xd;       // [K / 32]
+    uint16_t* y;           // [N]
+    uint16_t* y2;          // [N] for W2
+    const float* bias;     // [N] or null (indexed by the row within its matrix)
+    const uint16_t* res;   // [N] or null (may alias y)
+    size_t row_bytes;
+    int K, N;
+};
+int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream);
 int launch_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd, hipStream_t stream);
 
 }  // namespace fa

@@ -40,6 +40,22 @@ __device__ __forceinline__ uint32_t ld16x2(const uint8_t* p) {
 }
 __device__ __forceinline__ uint32_t ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
+// N 4-byte words from a 2-byte aligned address p, with aligned dword loads: from p itself
+// when it is 4-byte aligned, else from p - 2 plus one 2-byte load of the tail, the words
+// realigned by v_alignbyte. Reads stay within [p - 2, p + 4N): the 2 bytes before p lie in
+// the same buffer (its base is 4-byte aligned and p is not).
+template <int N>
+__device__ __forceinline__ void ld_span_a2(const uint8_t* p, uint32_t (&out)[N]) {
+    const bool mis = (reinterpret_cast<uintptr_t>(p) & 2) != 0;
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(p - (mis ? 2 : 0));
+    uint32_t t[N + 1];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = a[i];
+    t[N] = mis ? (uint32_t)*reinterpret_cast<const uint16_t*>(a + N) : 0u;
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = mis ? __builtin_amdgcn_alignbyte(t[i + 1], t[i], 2) : t[i];
+}
+
 // One 32-value block of a weight row: byte l of u (unsigned) maps to ws[l/16] * byte + c[l/16].
 // Offsets of the signed kinds are folded into c (c = -off * ws, exact: off is a power of 2),
 // the mins of Q2_K / Q4_K / Q5_K are c = -min.
@@ -92,14 +108,9 @@ __device__ __forceinline__ void load_wraw(const uint8_t* row, int blk, WRaw& r) 
     } else if constexpr (KIND == kKqQ3K) {
         const uint8_t* b = row + (size_t)sb * 110;
         const int h = j >> 2;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            r.a[w] = ld16x2(b + 32 + 32 * h + 4 * w);
-            r.b[w] = ld16x2(b + 4 * w);
-        }
-        r.s[0] = ld16x2(b + 96);
-        r.s[1] = ld16x2(b + 100);
-        r.s[2] = ld16x2(b + 104);
+        ld_span_a2<8>(b + 32 + 32 * h, r.a);
+        ld_span_a2<8>(b, r.b);
+        ld_span_a2<3>(b + 96, r.s);
         r.d = ld16(b + 108);
     } else if constexpr (KIND == kKqQ4K || KIND == kKqQ5K) {
         constexpr bool Q5 = KIND == kKqQ5K;
@@ -117,17 +128,13 @@ __device__ __forceinline__ void load_wraw(const uint8_t* row, int blk, WRaw& r) 
     } else if constexpr (KIND == kKqQ6K) {
         const uint8_t* b = row + (size_t)sb * 210;
         const int h = j >> 2, p = j & 3;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            r.a[w] = ld16x2(b + 64 * h + 32 * (p & 1) + 4 * w);
-            r.b[w] = ld16x2(b + 128 + 32 * h + 4 * w);
-        }
+        ld_span_a2<8>(b + 64 * h + 32 * (p & 1), r.a);
+        ld_span_a2<8>(b + 128 + 32 * h, r.b);
         r.s[0] = ld16(b + 192 + 8 * h + 2 * p);
         r.d = ld16(b + 208);
     } else {  // Q8_0
         const uint8_t* b = row + (size_t)blk * 34;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) r.a[w] = ld16x2(b + 2 + 4 * w);
+        ld_span_a2<8>(b + 2, r.a);
         r.d = ld16(b);
     }
 }
@@ -431,6 +438,54 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
     }
 }
 
+// Decode GEMV with int8 activations (gemvQ8, hpc_k_quants.cu:440-700, 904-931): y = W x for
+// one quantised activation vector, one wave per weight row (rows >= N from W2 into y2).
+// Lane l takes the 32-value blocks l, l + 64, ... of the row; per block the integer dot
+// products of each 16-value half with v_dot4_i32_i8 (exact, as the reference's dp4a) and
+// the activation sums for the min / offset term, scaled in fp32; a wave sum; the storeQ8
+// epilogue. HBM-bound: every weight byte is read once.
+template <int KIND>
+__global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
+    const int lane = threadIdx.x & 63;
+    int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int rows = p.W2 ? 2 * p.N : p.N;
+    if (row >= rows) return;  // the whole wave
+    const uint8_t* W = p.W;
+    uint16_t* y = p.y;
+    if (p.W2 && row >= p.N) {
+        W = p.W2;
+        y = p.y2;
+        row -= p.N;
+    }
+    const uint8_t* wrow = W + (size_t)row * p.row_bytes;
+    const int nblk = p.K / 32;
+    float acc = 0.0f;
+    for (int blk = lane; blk < nblk; blk += 64) {
+        WRaw r;
+        load_wraw<KIND>(wrow, blk, r);
+        const uint4 xa = *reinterpret_cast<const uint4*>(p.xq + 32 * blk);
+        const uint4 xb = *reinterpret_cast<const uint4*>(p.xq + 32 * blk + 16);
+        const float dx = p.xd[blk];
+        WBlock b;
+        decode_wraw<KIND>(r, blk, b);
+        const int x[8] = {(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w, (int)xb.x, (int)xb.y, (int)xb.z, (int)xb.w};
+        int dot[2] = {0, 0}, xs[2] = {0, 0};
+        float cs[2] = {b.c[0], b.c[1]};
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            // Q8_0: the signed codes themselves (u = q + 128 would not fit a signed byte)
+            const int wv = KIND == kKqQ80 ? (int)r.a[w] : (int)b.u[w];
+            dot[w >> 2] = __builtin_amdgcn_sdot4(wv, x[w], dot[w >> 2], false);
+            xs[w >> 2] = __builtin_amdgcn_sdot4(0x01010101, x[w], xs[w >> 2], false);
+        }
+        if (KIND == kKqQ80) cs[0] = cs[1] = 0.0f;
+        acc += dx * (b.ws[0] * (float)dot[0] + cs[0] * (float)xs[0] + b.ws[1] * (float)dot[1] + cs[1] * (float)xs[1]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
+}
+
 // quantize_x_q8_kernel semantics (hpc_k_quants.cu:386-400): 32 lanes per 32-value block,
 // d = amax / 127 (correctly rounded), inv = d > 0 ? 1 / d : 0, q = clamp(rne(x * inv), +-127)
 __global__ __launch_bounds__(256) void quantize_q8_rows_kernel(const uint16_t* __restrict__ x, int K,
@@ -486,6 +541,21 @@ int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
     if (shape == 2) return launch_kq_shape<2, 2, 2, 2>(kind, p, stream);
     if (shape == 4) return launch_kq_shape<2, 4, 2, 1>(kind, p, stream);
     return launch_kq_shape<2, 2, 1, 1>(kind, p, stream);
+}
+
+int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream) {
+    const int rows = p.W2 ? 2 * p.N : p.N;
+    const dim3 grid((rows + 3) / 4), block(256);
+    switch (kind) {
+        case kKqQ2K: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ2K>, grid, block, 0, stream, p); break;
+        case kKqQ3K: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ3K>, grid, block, 0, stream, p); break;
+        case kKqQ4K: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ4K>, grid, block, 0, stream, p); break;
+        case kKqQ5K: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ5K>, grid, block, 0, stream, p); break;
+        case kKqQ6K: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ6K>, grid, block, 0, stream, p); break;
+        case kKqQ80: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ80>, grid, block, 0, stream, p); break;
+        default: return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, float* xd, hipStream_t stream) {

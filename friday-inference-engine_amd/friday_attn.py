@@ -60,6 +60,7 @@ API = [
     ("friday_quantize_q8_rows", _I, [_P, _I, _I, _P, _P, _P]),
     ("friday_gemm_q8_supported", _I, [_I, _I]),
     ("friday_gemm_q8", _I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _P]),
+    ("friday_gemv_q8", _I, [_I, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
 ]
 
 _lib = None
@@ -412,3 +413,9 @@ def gemmQ8Supported(kind, K) -> bool:
 def gemmQ8(kind, W, xq, xd, T, K, N, Y, ldy, stream=None, bias=None, res=None):
     _check(load().friday_gemm_q8(kind, _ptr(W), _ptr(xq), _ptr(xd), T, K, N, _ptr(Y), ldy, stream, _ptr(bias),
                                  _ptr(res)))
+
+
+def gemvQ8(kind, W, xq, xd, K, N, y, stream=None, W2=None, y2=None, bias=None, res=None):
+    """friday_hpc::gemvQ8 with the activation scratch (xq, xd) passed explicitly."""
+    _check(load().friday_gemv_q8(kind, _ptr(W), _ptr(xq), _ptr(xd), K, N, _ptr(y), stream, _ptr(W2), _ptr(y2),
+                                 _ptr(bias), _ptr(res)))

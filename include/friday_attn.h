@@ -214,6 +214,17 @@ int friday_gemm_q8_supported(int kind, int K);
  * test bar (test_prefill_gemm.cu:111-129: rel-L2 < 1e-3, max |diff| < 1e-2 RMS). */
 int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
                    int ldy, void* stream, const float* bias, const uint16_t* res);
+/* Replaces friday_hpc::gemvQ8 (hpc_k_quants.h:64-68, hpc_k_quants.cu:904-931), the decode
+ * GEMV with int8 activations (the O-projection after attention, transformer.cpp:1057-1059):
+ * y[n] = sum_k W[n][k] x[k] for one vector x given as xq [K] int8 and xd [K/32] fp32 (the
+ * output of friday_quantize_q8_rows with rows = 1; the reference keeps them in a hidden
+ * scratch filled by quantizeQ8). If W2, rows of W2 go to y2 in the same launch. Epilogue
+ * as friday_gemm_q8 with bias[n] and res[n] (res may alias y), applied to y and y2 alike
+ * (storeQ8, hpc_k_quants.cu:422-437). Per 32 values the integer dot products are exact
+ * (v_dot4_i32_i8) and scaled in fp32. K a multiple of 256 (of 32 for Q8_0); W, W2 4-byte
+ * aligned, xq 16-byte aligned. */
+int friday_gemv_q8(int kind, const void* W, const int8_t* xq, const float* xd, int K, int N, uint16_t* y,
+                   void* stream, const void* W2, uint16_t* y2, const float* bias, const uint16_t* res);
 
 #ifdef __cplusplus
 }

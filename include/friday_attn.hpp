@@ -1,6 +1,8 @@
 // Header-only C++17 drop-in for the reference's friday_attn:: launchers
-// (attention_kernels.h:7-52) and for the direct ropeStoreKvKernel / storeKvQ8Kernel
-// launches of transformer.cpp, implemented on the friday_attn C ABI.
+// (attention_kernels.h:7-52), the direct ropeStoreKvKernel / storeKvQ8Kernel launches of
+// transformer.cpp, and the int8-activation matmuls on either side of attention
+// (friday_hpc::quantizeQ8 / quantizeQ8Rows / gemvQ8, hpc_k_quants.h:39-68;
+// friday_prefill::gemmQ8, prefill_kernels.h:15-25), implemented on the friday_attn C ABI.
 //
 // Same names, argument order and meaning; tensors are taken as void pointers so
 // that half* / __half* / uint16_t* arguments all convert. Errors throw
@@ -101,5 +103,73 @@ inline void storeKvQ8(const void* k, const void* v, int8_t* k_layer, void* k_sca
 }
 
 }  // namespace friday_attn
+
+// ---- int8-activation matmuls: hpc_k_quants.h:39-68 and prefill_kernels.h:15-25
+namespace friday_hpc {
+
+enum class Q8Kind { None, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0 };  // codes = FA_KQ_*
+
+namespace detail {
+struct Q8Scratch {
+    int8_t* xq = nullptr;
+    float* xd = nullptr;
+    int cap = 0;
+};
+inline Q8Scratch& scratch() {
+    static Q8Scratch s;
+    return s;
+}
+}  // namespace detail
+
+// The activation scratch shared by quantizeQ8 and gemvQ8 (hpc_k_quants.h:51-57): allocate
+// it for vectors of up to K values before any HIP graph capture.
+inline void ensureQ8Scratch(int K, hipStream_t) {
+    auto& s = detail::scratch();
+    if (K <= s.cap) return;
+    if (s.xq) (void)hipFree(s.xq);
+    if (s.xd) (void)hipFree(s.xd);
+    const int cap = (K + 255) / 256 * 256;
+    if (hipMalloc(reinterpret_cast<void**>(&s.xq), (size_t)cap) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&s.xd), (size_t)cap / 32 * sizeof(float)) != hipSuccess)
+        throw std::runtime_error("ensureQ8Scratch: hipMalloc failed");
+    s.cap = cap;
+}
+inline void quantizeQ8(const void* x, int K, hipStream_t stream) {
+    ensureQ8Scratch(K, stream);
+    friday_attn::detail::check(
+        friday_quantize_q8_rows(friday_attn::detail::h(x), 1, K, detail::scratch().xq, detail::scratch().xd, stream));
+}
+inline void quantizeQ8Rows(const void* x, int rows, int K, int8_t* xq, float* xd, hipStream_t stream) {
+    friday_attn::detail::check(friday_quantize_q8_rows(friday_attn::detail::h(x), rows, K, xq, xd, stream));
+}
+inline bool gemvQ8Supported(Q8Kind k) { return k != Q8Kind::None; }
+inline void gemvQ8(Q8Kind kind, const void* W, void* y, int K, int N, hipStream_t stream, const void* W2 = nullptr,
+                   void* y2 = nullptr, const float* bias = nullptr, const void* res = nullptr) {
+    if (!gemvQ8Supported(kind)) {
+        std::fprintf(stderr, "gemvQ8: unsupported type\n");
+        std::abort();
+    }
+    friday_attn::detail::check(friday_gemv_q8((int)kind, W, detail::scratch().xq, detail::scratch().xd, K, N,
+                                              friday_attn::detail::h(y), stream, W2, friday_attn::detail::h(y2),
+                                              bias, friday_attn::detail::h(res)));
+}
+
+}  // namespace friday_hpc
+
+namespace friday_prefill {
+
+inline bool gemmQ8Supported(friday_hpc::Q8Kind kind, int K) { return friday_gemm_q8_supported((int)kind, K) != 0; }
+inline void gemmQ8(friday_hpc::Q8Kind kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N,
+                   void* Y, int ldy, hipStream_t stream, const float* bias = nullptr, const void* res = nullptr) {
+    if (!gemmQ8Supported(kind, K)) {  // prefill_kernels.cu:344-347
+        std::fprintf(stderr, "gemmQ8: unsupported type, K=%d or device\n", K);
+        std::abort();
+    }
+    friday_attn::detail::check(friday_gemm_q8((int)kind, W, xq, xd, T, K, N, friday_attn::detail::h(Y), ldy, stream,
+                                              bias, friday_attn::detail::h(res)));
+}
+
+}  // namespace friday_prefill
+
 
 #endif  // FRIDAY_ATTN_HPP

@@ -18,7 +18,7 @@ FAKE = 0x1000  # non-null pointer value: every call below must fail before touch
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(friday_(?:attn|gemm|quantize|q8)_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(friday_(?:attn|gemm|gemv|quantize|q8)_\w+)\s*\(", text)))
 
 
 def test_header_and_binding_agree(fa):
@@ -134,10 +134,13 @@ def test_error_message_is_thread_local(fa):
 
 
 def test_cpp_shim_compiles():
-    """include/friday_attn.hpp (the friday_attn:: drop-in) compiles as C++17 host code."""
+    """include/friday_attn.hpp (the friday_attn:: / friday_hpc:: / friday_prefill:: drop-in)
+    compiles as C++17 host code."""
     import subprocess
     import tempfile
-    src = '#include "friday_attn.hpp"\nint main() { return friday_attn::decodeAttentionFitsSharedMemory(10) ? 0 : 1; }\n'
+    src = ('#include "friday_attn.hpp"\nint main() { return friday_attn::decodeAttentionFitsSharedMemory(10) && '
+           'friday_prefill::gemmQ8Supported(friday_hpc::Q8Kind::Q4_K, 256) && '
+           'friday_hpc::gemvQ8Supported(friday_hpc::Q8Kind::Q8_0) ? 0 : 1; }\n')
     with tempfile.TemporaryDirectory() as d:
         f = os.path.join(d, "t.cpp")
         open(f, "w").write(src)
@@ -168,3 +171,16 @@ def test_gemm_q8_validation(fa):
     # activation quantiser: K multiple of 32
     assert L.friday_quantize_q8_rows(FAKE, 2, 48, FAKE, FAKE, None) == fa.FA_ERR_INVALID
     assert L.friday_quantize_q8_rows(FAKE, 0, 64, FAKE, FAKE, None) == fa.FA_OK
+
+
+def test_gemv_q8_validation(fa):
+    L = fa.load()
+    # K: a multiple of 256 (of 32 for Q8_0); unknown kind
+    assert L.friday_gemv_q8(fa.Q4_K, FAKE, FAKE, FAKE, 1000, 64, FAKE, None, None, None, None, None) == \
+        fa.FA_ERR_UNSUPPORTED
+    assert L.friday_gemv_q8(0, FAKE, FAKE, FAKE, 1024, 64, FAKE, None, None, None, None, None) == fa.FA_ERR_UNSUPPORTED
+    # W2 without y2, N <= 0, misaligned W
+    assert L.friday_gemv_q8(fa.Q8_0, FAKE, FAKE, FAKE, 96, 64, FAKE, None, FAKE, None, None, None) == fa.FA_ERR_INVALID
+    assert L.friday_gemv_q8(fa.Q8_0, FAKE, FAKE, FAKE, 96, 0, FAKE, None, None, None, None, None) == fa.FA_ERR_INVALID
+    assert L.friday_gemv_q8(fa.Q8_0, FAKE + 2, FAKE, FAKE, 96, 8, FAKE, None, None, None, None, None) == \
+        fa.FA_ERR_INVALID

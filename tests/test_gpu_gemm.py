@@ -97,3 +97,64 @@ def test_model_projection_shapes(gpu, oracle, kind, K, N):
     rows = np.unique(np.concatenate([[0, 1, 127, 128, N - 1], rng.choice(N, 43, replace=False)]))
     ref, _ = oracle.gemm_q8(kind, np.ascontiguousarray(W[rows]), xq, xd, T, K, len(rows))
     assert_gemm_close(got[:, rows], ref.view(np.float16).astype(np.float32), f"{KQ_KINDS[kind][0]} K={K} N={N}")
+
+
+# ---- decode GEMV (friday_gemv_q8): test_kquant_kernels.cu shapes (K = 1024, N = 64) per kind,
+# the O-projection of the decode step (transformer.cpp:1057-1059) at Qwen2.5-32B shapes with the
+# residual in place, and the two-matrix launch (W2 -> y2) with a bias.
+
+def run_gemv(fa, kind, W, x, K, N, W2=None, bias=None, res=None):
+    dW = fa.DeviceBuffer.from_array(W)
+    dW2 = fa.DeviceBuffer.from_array(W2) if W2 is not None else None
+    dx = fa.DeviceBuffer.from_array(x)
+    dq, dd = fa.DeviceBuffer(K), fa.DeviceBuffer(K // 32 * 4)
+    fa.quantizeQ8Rows(dx, 1, K, dq, dd)
+    dy = fa.DeviceBuffer.from_array(res if res is not None else np.zeros(N, np.uint16))
+    dy2 = fa.DeviceBuffer.from_array(np.zeros(N, np.uint16)) if W2 is not None else None
+    db = fa.DeviceBuffer.from_array(bias) if bias is not None else None
+    fa.gemvQ8(kind, dW, dq, dd, K, N, dy, W2=dW2, y2=dy2, bias=db, res=dy if res is not None else None)
+    fa.Hip.sync()
+    y = dy.download(N, np.uint16)
+    y2 = dy2.download(N, np.uint16) if W2 is not None else None
+    return y, y2, dq.download((1, K), np.int8), dd.download((1, K // 32), np.float32)
+
+
+@pytest.mark.parametrize("kind", sorted(KQ_KINDS))
+def test_gemv_reference_kernel_shapes(gpu, oracle, kind):
+    fa = gpu
+    K, N = 1024, 64
+    rng = np.random.default_rng(20261107 + kind)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((1, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    y, _, xq, xd = run_gemv(fa, kind, W, x, K, N)
+    ref, _ = oracle.gemm_q8(kind, W, xq, xd, 1, K, N)
+    assert_gemm_close(y.view(np.float16).astype(np.float32), ref.view(np.float16).astype(np.float32),
+                      f"gemv {KQ_KINDS[kind][0]}")
+
+
+@pytest.mark.parametrize("kind", [3, 5, 6])
+def test_gemv_o_projection_residual(gpu, oracle, kind):
+    fa = gpu
+    K = N = 5120
+    rng = np.random.default_rng(kind + 77)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((1, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    res = rng.standard_normal(N, dtype=np.float32).astype(np.float16).view(np.uint16)
+    y, _, xq, xd = run_gemv(fa, kind, W, x, K, N, res=res)
+    ref, _ = oracle.gemm_q8(kind, W, xq, xd, 1, K, N, res=res[None])
+    assert_gemm_close(y.view(np.float16).astype(np.float32), ref[0].view(np.float16).astype(np.float32), "o_proj")
+
+
+def test_gemv_two_matrices_bias(gpu, oracle):
+    fa = gpu
+    kind, K, N = 1, 2048, 300
+    rng = np.random.default_rng(9)
+    W, W2 = kq_random_weights(rng, kind, N, K), kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((1, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    y, y2, xq, xd = run_gemv(fa, kind, W, x, K, N, W2=W2, bias=bias)
+    r1, _ = oracle.gemm_q8(kind, W, xq, xd, 1, K, N, bias=bias)
+    r2, _ = oracle.gemm_q8(kind, W2, xq, xd, 1, K, N, bias=bias)
+    f = lambda a: a.view(np.float16).astype(np.float32)  # noqa: E731
+    assert_gemm_close(f(y), f(r1[0]), "y")
+    assert_gemm_close(f(y2), f(r2[0]), "y2")
