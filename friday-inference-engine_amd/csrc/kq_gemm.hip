@@ -486,6 +486,75 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
     if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
 }
 
+// LDS-staged decode GEMV: a workgroup takes 4 consecutive weight rows (contiguous bytes),
+// copies them into LDS with one burst of global_load_lds_dword (every copy in flight at
+// once, no registers), then each wave computes its row as kq_gemv_kernel does, reading the
+// blocks from LDS. Rows start in LDS at the same offsets mod 4 as in memory, so the
+// 2-byte aligned kinds use the same realigning loads.
+typedef __attribute__((address_space(3))) unsigned char gv_lds_u8;
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, gv_lds_u8* lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off),
+                 "s"(base)
+                 : "memory");
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void kq_gemv_lds_kernel(KqGemvParams p) {
+    extern __shared__ __align__(16) unsigned char rows_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gpm = (p.N + 3) / 4;  // row groups per matrix
+    int g = blockIdx.x;
+    const uint8_t* W = p.W;
+    uint16_t* y = p.y;
+    if (g >= gpm) {
+        g -= gpm;
+        W = p.W2;
+        y = p.y2;
+    }
+    const int n0 = g * 4;
+    const int nrows = min(4, p.N - n0);
+    const uint32_t span = (uint32_t)(nrows * p.row_bytes);  // a multiple of 4 bytes (4 rows or up to the end)
+    const uint8_t* src = W + (size_t)n0 * p.row_bytes;      // 4-byte aligned: n0 is a multiple of 4
+    gv_lds_u8* lds = (gv_lds_u8*)rows_lds;
+    // wave w copies 256-byte pieces w, w + 4, ...; lane l moves bytes 4l..4l+3 of a piece
+    const uint32_t pieces = (span + 255) / 256;
+    for (uint32_t i = wave; i < pieces; i += 4) {
+        const uint32_t off = min(256 * i + 4 * lane, span - 4);  // the tail re-reads the last word
+        dma4(src, off, lds + 256 * i);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (wave >= nrows) return;
+    const int row = n0 + wave;
+    const unsigned char* wrow = rows_lds + (size_t)wave * p.row_bytes;
+    const int nblk = p.K / 32;
+    float acc = 0.0f;
+    for (int blk = lane; blk < nblk; blk += 64) {
+        WRaw r;
+        load_wraw<KIND>(wrow, blk, r);
+        const uint4 xa = *reinterpret_cast<const uint4*>(p.xq + 32 * blk);
+        const uint4 xb = *reinterpret_cast<const uint4*>(p.xq + 32 * blk + 16);
+        const float dx = p.xd[blk];
+        WBlock b;
+        decode_wraw<KIND>(r, blk, b);
+        const int x[8] = {(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w, (int)xb.x, (int)xb.y, (int)xb.z, (int)xb.w};
+        int dot[2] = {0, 0}, xs[2] = {0, 0};
+        float cs[2] = {b.c[0], b.c[1]};
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const int wv = KIND == kKqQ80 ? (int)r.a[w] : (int)b.u[w];
+            dot[w >> 2] = __builtin_amdgcn_sdot4(wv, x[w], dot[w >> 2], false);
+            xs[w >> 2] = __builtin_amdgcn_sdot4(0x01010101, x[w], xs[w >> 2], false);
+        }
+        if (KIND == kKqQ80) cs[0] = cs[1] = 0.0f;
+        acc += dx * (b.ws[0] * (float)dot[0] + cs[0] * (float)xs[0] + b.ws[1] * (float)dot[1] + cs[1] * (float)xs[1]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
+}
+
 // quantize_x_q8_kernel semantics (hpc_k_quants.cu:386-400): 32 lanes per 32-value block,
 // d = amax / 127 (correctly rounded), inv = d > 0 ? 1 / d : 0, q = clamp(rne(x * inv), +-127)
 __global__ __launch_bounds__(256) void quantize_q8_rows_kernel(const uint16_t* __restrict__ x, int K,
@@ -543,8 +612,28 @@ int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
     return launch_kq_shape<2, 2, 1, 1>(kind, p, stream);
 }
 
+// The LDS-staged GEMV when four rows fit in 64 KiB (two workgroups per CU), else one wave
+// per row straight from memory. FRIDAY_GEMV_LDS = 0 forces the direct kernel.
 int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream) {
+    static const bool lds_ok = [] {
+        const char* e = std::getenv("FRIDAY_GEMV_LDS");
+        return !(e && *e == '0');
+    }();
     const int rows = p.W2 ? 2 * p.N : p.N;
+    const size_t lds = ((4 * p.row_bytes + 255) / 256) * 256;
+    if (lds_ok && lds <= 65536) {
+        const dim3 grid(((p.N + 3) / 4) * (p.W2 ? 2 : 1)), block(256);
+        switch (kind) {
+            case kKqQ2K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ2K>, grid, block, lds, stream, p); break;
+            case kKqQ3K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ3K>, grid, block, lds, stream, p); break;
+            case kKqQ4K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ4K>, grid, block, lds, stream, p); break;
+            case kKqQ5K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ5K>, grid, block, lds, stream, p); break;
+            case kKqQ6K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ6K>, grid, block, lds, stream, p); break;
+            case kKqQ80: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ80>, grid, block, lds, stream, p); break;
+            default: return -2;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     const dim3 grid((rows + 3) / 4), block(256);
     switch (kind) {
         case kKqQ2K: hipLaunchKernelGGL(kq_gemv_kernel<kKqQ2K>, grid, block, 0, stream, p); break;
