@@ -361,6 +361,51 @@ def gemv_config(cx, kind, K, N, what, steps, warmup):
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def layer_block_config(cx, S, L, steps, warmup):
+    """The attention block of one decode layer at the headline shape, as gpuLayerFused runs it
+    (transformer.cpp:1046-1059): decode step (RoPE + append + attention), quantizeQ8 of the
+    output, O-projection gemvQ8 (Q4_K, 5120 x 5120) with the residual in place; 64 layers,
+    one HIP graph. HBM bytes per layer = K/V of the context + the O-projection weights."""
+    import numpy as np
+
+    fa = cx.fa
+    Hq, Hkv, d = 40, 8, 128
+    H = Hq * d
+    dl = DecodeLayers(cx, S, L, Hq, Hkv, d)
+    bb, vals, offs = KQ_LAYOUT[3]
+    rng = np.random.default_rng(3)
+    W = rng.integers(0, 256, size=(H, H // vals, bb), dtype=np.uint8)
+    for off in offs:
+        W[:, :, off:off + 2] = rng.uniform(1e-3, 1e-2, size=(H, H // vals)).astype(np.float16).view(
+            np.uint8).reshape(H, H // vals, 2)
+    W = W.reshape(H, -1)
+    wb = W.nbytes
+    dW = fa.DeviceBuffer(L * wb)
+    for l in range(L):
+        dW.upload(W, l * wb)
+    x = fa.DeviceBuffer(L * H * 2)
+    cx.fill(x, L * H, 21)
+    xq, xd = fa.DeviceBuffer(H), fa.DeviceBuffer(H // 32 * 4)
+
+    def run():
+        for l in range(L):
+            q, kn, vn, kc, vc, out = dl.ptrs(l)
+            fa.decodeStep(q, kn, vn, kc, vc, out, dl.pos, 0, S, Hq, Hkv, d, dl.table, 1, dl.ws, cx.stream.s)
+            fa.quantizeQ8Rows(out, 1, H, xq, xd, cx.stream.s)
+            xl = x.ptr + l * H * 2
+            fa.gemvQ8(fa.Q4_K, dW.ptr + l * wb, xq, xd, H, H, xl, cx.stream.s, res=xl)
+
+    ms = cx.timed(run, steps, warmup)
+    dl.free()
+    for b in (dW, x, xq, xd):
+        b.free()
+    us = ms * 1e3 / L
+    hbm = 2 * S * Hkv * d * 2 + wb
+    return {"config": "decode layer attention block", "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
+            "o_proj": f"Q4_K {H}x{H}", "us_per_layer": round(us, 2), "hbm_MB_per_layer": round(hbm / 1e6, 1),
+            "GBps": round(hbm / (us * 1e-6) / 1e9, 1), "hbm_frac": round(hbm / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def q8_config(cx, S, L, steps, warmup):
     """int8 KV (FRIDAY --kv q8) at the headline shape: one friday_attn_decode_step_q8 per layer."""
     import numpy as np
@@ -454,7 +499,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
-    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm", "layer"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other BASELINE configs")
     args = ap.parse_args()
 
@@ -482,6 +527,7 @@ def main():
             lines.append(gemm_config(cx, *case, args.steps, args.warmup))
         for case in GEMV_CASES:
             lines.append(gemv_config(cx, *case, args.steps, args.warmup))
+        lines.append(layer_block_config(cx, 32768, 64, args.steps, args.warmup))
         for rec in lines:
             print(json.dumps(rec), flush=True)
     if args.config == "q8":
@@ -491,6 +537,8 @@ def main():
     if args.config == "prefill":
         for p0 in (0, 1024, 2048, 4096, 7680):
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup)), flush=True)
+    if args.config == "layer":
+        print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
     if args.config == "gemm":
         for case in GEMM_CASES:
             print(json.dumps(gemm_config(cx, *case, args.steps, args.warmup)), flush=True)
