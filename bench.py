@@ -361,11 +361,12 @@ def gemv_config(cx, kind, K, N, what, steps, warmup):
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def layer_block_config(cx, S, L, steps, warmup):
+def layer_block_config(cx, S, L, steps, warmup, fused=False):
     """The attention block of one decode layer at the headline shape, as gpuLayerFused runs it
     (transformer.cpp:1046-1059): decode step (RoPE + append + attention), quantizeQ8 of the
     output, O-projection gemvQ8 (Q4_K, 5120 x 5120) with the residual in place; 64 layers,
-    one HIP graph. HBM bytes per layer = K/V of the context + the O-projection weights."""
+    one HIP graph. HBM bytes per layer = K/V of the context + the O-projection weights.
+    fused: the quantisation runs in the decode step's merge epilogue (friday_attn_decode_step_quant)."""
     import numpy as np
 
     fa = cx.fa
@@ -390,8 +391,12 @@ def layer_block_config(cx, S, L, steps, warmup):
     def run():
         for l in range(L):
             q, kn, vn, kc, vc, out = dl.ptrs(l)
-            fa.decodeStep(q, kn, vn, kc, vc, out, dl.pos, 0, S, Hq, Hkv, d, dl.table, 1, dl.ws, cx.stream.s)
-            fa.quantizeQ8Rows(out, 1, H, xq, xd, cx.stream.s)
+            if fused:
+                fa.decodeStepQuant(q, kn, vn, kc, vc, out, xq, xd, dl.pos, 0, S, Hq, Hkv, d, dl.table, 1, dl.ws,
+                                   cx.stream.s)
+            else:
+                fa.decodeStep(q, kn, vn, kc, vc, out, dl.pos, 0, S, Hq, Hkv, d, dl.table, 1, dl.ws, cx.stream.s)
+                fa.quantizeQ8Rows(out, 1, H, xq, xd, cx.stream.s)
             xl = x.ptr + l * H * 2
             fa.gemvQ8(fa.Q4_K, dW.ptr + l * wb, xq, xd, H, H, xl, cx.stream.s, res=xl)
 
@@ -401,7 +406,7 @@ def layer_block_config(cx, S, L, steps, warmup):
         b.free()
     us = ms * 1e3 / L
     hbm = 2 * S * Hkv * d * 2 + wb
-    return {"config": "decode layer attention block", "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
+    return {"config": "decode layer attention block" + (" (quantize fused into the step)" if fused else ""), "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
             "o_proj": f"Q4_K {H}x{H}", "us_per_layer": round(us, 2), "hbm_MB_per_layer": round(hbm / 1e6, 1),
             "GBps": round(hbm / (us * 1e-6) / 1e9, 1), "hbm_frac": round(hbm / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
@@ -528,6 +533,7 @@ def main():
         for case in GEMV_CASES:
             lines.append(gemv_config(cx, *case, args.steps, args.warmup))
         lines.append(layer_block_config(cx, 32768, 64, args.steps, args.warmup))
+        lines.append(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True))
         for rec in lines:
             print(json.dumps(rec), flush=True)
     if args.config == "q8":
@@ -539,6 +545,7 @@ def main():
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup)), flush=True)
     if args.config == "layer":
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
+        print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True)), flush=True)
     if args.config == "gemm":
         for case in GEMM_CASES:
             print(json.dumps(gemm_config(cx, *case, args.steps, args.warmup)), flush=True)

@@ -271,7 +271,8 @@ namespace {
 int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint16_t* v, const void* k_layer,
                        const void* v_layer, const uint16_t* k_scale, const uint16_t* v_scale, uint16_t* out,
                        const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads, int head_dim,
-                       const float* rope_table, int neox, void* workspace, size_t workspace_bytes, void* stream) {
+                       const float* rope_table, int neox, void* workspace, size_t workspace_bytes, void* stream,
+                       int8_t* out_q = nullptr, float* out_d = nullptr) {
     if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
     if (!q || !k || !v || !k_layer || !v_layer || !out || !rope_table || max_ctx <= 0)
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
@@ -283,6 +284,7 @@ int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint
     p.q = q; p.k = k_layer; p.v = v_layer; p.d_pos = d_pos; p.seq_len = d_pos ? 0 : pos + 1; p.max_seq = max_ctx;
     p.k_scale = k_scale; p.v_scale = v_scale;
     p.out = out; p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = G; p.ngb = (G + 15) / 16;
+    p.out_q = out_q; p.out_d = out_d;
     p.kv_dim = num_kv_heads * head_dim;
     p.min_chunk = fa::min_chunk();
     p.max_splits = fa::splits_for(num_kv_heads, p.ngb);
@@ -317,6 +319,20 @@ int friday_attn_decode_step_q8(uint16_t* q, const uint16_t* k, const uint16_t* v
     return decode_step_common("decode_step_q8", q, k, v, k_layer, v_layer, k_scale, v_scale, out, d_pos, pos,
                               max_ctx, num_heads, num_kv_heads, head_dim, rope_table, neox, workspace,
                               workspace_bytes, stream);
+}
+
+int friday_attn_decode_step_quant(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer,
+                                  uint16_t* v_layer, uint16_t* out, int8_t* out_q, float* out_d, const int* d_pos,
+                                  int pos, int max_ctx, int num_heads, int num_kv_heads, int head_dim,
+                                  const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    const char* w = "decode_step_quant";
+    if (!out_q || !out_d) return fail(FA_ERR_INVALID, "%s: out_q and out_d required", w);
+    if (reinterpret_cast<uintptr_t>(out_q) % 4 || reinterpret_cast<uintptr_t>(out_d) % 4)
+        return fail(FA_ERR_INVALID, "%s: out_q / out_d must be 4-byte aligned", w);
+    return decode_step_common(w, q, k, v, k_layer, v_layer, nullptr, nullptr, out, d_pos, pos, max_ctx, num_heads,
+                              num_kv_heads, head_dim, rope_table, neox, workspace, workspace_bytes, stream, out_q,
+                              out_d);
 }
 
 // ---------------- prefill ----------------

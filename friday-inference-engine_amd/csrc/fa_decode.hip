@@ -133,6 +133,35 @@ __device__ __forceinline__ void quant_chunk16(const h8* x, u4& q, float& scale, 
 // bypass the caches: in the fused path other workgroups of this launch wrote them
 // through to memory just before.
 // NB: partial rows per thread loaded in one round trip (8 or 32, >= nsp when possible)
+// Writes 4 consecutive output values of one head row (columns 4c..4c+3) and, when the
+// caller asked for it, their int8 form: per 32 values d = amax / 127, q = clamp(rne(x / d)),
+// exactly as quantize_x_q8_kernel (hpc_k_quants.cu:386-400) applied to the fp16 output.
+// The 8 lanes holding one 32-value block (consecutive c, same row) must call it together.
+__device__ __forceinline__ void store_out4(const DecodeParams& p, size_t row, int D, int c, h4 o) {
+    reinterpret_cast<h4*>(p.out + row * D)[c] = o;
+    if (p.out_q) {
+        float v[4], amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = (float)o[i];
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+#pragma unroll
+        for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+        const float d = amax / 127.0f;
+        const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int q = (int)__builtin_rintf(v[i] * inv);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            packed |= (uint32_t)(q & 0xFF) << (8 * i);
+        }
+        *reinterpret_cast<uint32_t*>(p.out_q + row * D + 4 * c) = packed;
+        if ((c & 7) == 0) p.out_d[(row * D + 4 * c) / 32] = d;
+    }
+}
+
 template <int D, int NB>
 __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
     constexpr int C4 = D / 4;
@@ -225,7 +254,7 @@ __device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp,
             h4 o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
-            reinterpret_cast<h4*>(p.out + orow * D)[c] = o;
+            store_out4(p, orow, D, c, o);
         }
         __syncthreads();  // LDS reused by the next pass
     }
@@ -297,7 +326,7 @@ __device__ void merge_short(const DecodeParams& p, size_t row0, int nh, int nsp,
             h4 o;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
-            reinterpret_cast<h4*>(p.out + (row0 + h0 + hh) * D)[c] = o;
+            store_out4(p, row0 + h0 + hh, D, c, o);
         }
         if (h0 + HB < nh) __syncthreads();  // LDS reused by the next pass
     }
@@ -683,7 +712,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
             h4 r;
 #pragma unroll
             for (int i = 0; i < 4; ++i) r[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
-            *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(p.out) + row * D + 4 * d4) = r;
+            store_out4(p, row, D, d4, r);
         } else {
             // written through to the device coherence point (sc1) for the merging workgroup
             const size_t slot = row * p.nsplit_grid + split;

@@ -58,6 +58,8 @@ struct DecodeParams {
     float* part_ml;            // [B*Hq][nsplit_grid][2]  (max in log2 units, sum)
     int* counters;             // fused merge: [B][Hkv*ngb] arrival counters (zero between launches); null: merge kernel
     uint16_t* out;             // [B][Hq*D]
+    int8_t* out_q;             // optional: out quantised per 32 values (quantizeQ8 rule), [B][Hq*D]
+    float* out_d;              // with out_q: the fp32 scales, [B][Hq*D/32]
     int Hq, Hkv, G, ngb, nsplit_grid, kv_dim;
     int single;                // 1: one split covers the whole context, no merge
     int min_chunk, max_splits; // split partition constants

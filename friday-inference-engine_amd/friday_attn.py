@@ -56,6 +56,8 @@ API = [
      [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_paged_decode_attention", _I,
      [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _SZ, _P]),
+    ("friday_attn_decode_step_quant", _I,
+     [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_q8_row_bytes", _SZ, [_I, _I]),
     ("friday_quantize_q8_rows", _I, [_P, _I, _I, _P, _P, _P]),
     ("friday_gemm_q8_supported", _I, [_I, _I]),
@@ -419,3 +421,14 @@ def gemvQ8(kind, W, xq, xd, K, N, y, stream=None, W2=None, y2=None, bias=None, r
     """friday_hpc::gemvQ8 with the activation scratch (xq, xd) passed explicitly."""
     _check(load().friday_gemv_q8(kind, _ptr(W), _ptr(xq), _ptr(xd), K, N, _ptr(y), stream, _ptr(W2), _ptr(y2),
                                  _ptr(bias), _ptr(res)))
+
+
+def decodeStepQuant(q, k, v, k_layer, v_layer, out, out_q, out_d, d_pos, pos, max_ctx, num_heads, num_kv_heads,
+                    head_dim, rope_table, neox, workspace, stream=None, workspace_bytes=None):
+    """decodeStep plus the int8 form of `out` (quantizeQ8) in the same launch."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_attn_decode_step_quant(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(v_layer), _ptr(out),
+                                                _ptr(out_q), _ptr(out_d), _ptr(d_pos), pos, max_ctx, num_heads,
+                                                num_kv_heads, head_dim, _ptr(rope_table), int(neox), _ptr(workspace),
+                                                workspace_bytes, stream))

@@ -144,6 +144,18 @@ int friday_attn_decode_step_q8(uint16_t* q, const uint16_t* k, const uint16_t* v
                                int head_dim, const float* rope_table, int neox, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* friday_attn_decode_step that also writes the attention output in the int8 activation
+ * format of the next matmul: out_q [Hq*d] int8 and out_d [Hq*d/32] fp32, bit for bit what
+ * friday_quantize_q8_rows(out, 1, Hq*d, ...) (quantizeQ8, hpc_k_quants.cu:386-400) gives.
+ * Replaces ropeStoreKvKernel + launchDecodeAttentionSplit + quantizeQ8 of gpuLayerFused
+ * (transformer.cpp:1046-1051, 1057) with one launch; the O-projection gemvQ8 then reads
+ * out_q / out_d (friday_gemv_q8). No reference counterpart as a single entry point. */
+int friday_attn_decode_step_quant(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer,
+                                  uint16_t* v_layer, uint16_t* out, int8_t* out_q, float* out_d, const int* d_pos,
+                                  int pos, int max_ctx, int num_heads, int num_kv_heads, int head_dim,
+                                  const float* rope_table, int neox, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* ---------------- prefill attention ----------------
  * friday_attn::prefillAttentionSupported / launchPrefillAttention
  * (attention_kernels.h:46-50, .cu:649-684): causal attention of T queries at

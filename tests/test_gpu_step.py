@@ -185,3 +185,44 @@ def test_step_q8_matches_three_launches(gpu, oracle, Hq, Hkv, d, S, max_ctx, neo
     assert np.array_equal(b1["k8"].download(k8.shape, np.int8), k8), "int8 k row vs oracle"
     assert np.array_equal(b1["vs"].download(vs.shape, np.uint16), vs), "v scales vs oracle"
     assert_close(as_f32(g1), oracle.decode_q8(qr[0], k8, ks, v8, vs, S, Hq, Hkv, d), f"q8 step S={S}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,d,S,max_ctx", [
+    (40, 8, 128, 32768, 32768),   # headline: 32 splits, short merge
+    (40, 8, 128, 1, 4096),        # one split: the decode workgroup writes out
+    (32, 8, 128, 20000, 20480),   # more than 8 splits per group
+    (14, 2, 64, 513, 1024),       # d = 64
+    (48, 1, 128, 2048, 2048),     # G = 48: three head blocks
+])
+def test_step_quant_matches_step_plus_quantize(gpu, oracle, Hq, Hkv, d, S, max_ctx):
+    """friday_attn_decode_step_quant = decode step + quantizeQ8 of its output, bit for bit."""
+    fa = gpu
+    rng = np.random.default_rng(S + Hq)
+    kv_dim = Hkv * d
+    kc, vc = f16(rng, (max_ctx, kv_dim)), f16(rng, (max_ctx, kv_dim))
+    q, k, v = f16(rng, (1, Hq * d), 2.0), f16(rng, (1, kv_dim)), f16(rng, (1, kv_dim))
+    dt = fa.DeviceBuffer.from_array(fa.rope_table_host(max_ctx, d, 1e6))
+    dpos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
+    ws_bytes = fa.splitAttentionWorkspaceBytes(Hq, max_ctx)
+    outs = []
+    for fused in (True, False):
+        b = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q, k=k, v=v, kc=kc, vc=vc).items()}
+        out = fa.DeviceBuffer(q.nbytes)
+        oq, od = fa.DeviceBuffer(Hq * d), fa.DeviceBuffer(Hq * d // 32 * 4)
+        ws = fa.DeviceBuffer(ws_bytes)
+        fa.decodeWorkspaceInit(ws)
+        if fused:
+            fa.decodeStepQuant(b["q"], b["k"], b["v"], b["kc"], b["vc"], out, oq, od, dpos, 0, max_ctx, Hq, Hkv, d,
+                               dt, 1, ws)
+        else:
+            fa.decodeStep(b["q"], b["k"], b["v"], b["kc"], b["vc"], out, dpos, 0, max_ctx, Hq, Hkv, d, dt, 1, ws)
+            fa.quantizeQ8Rows(out, 1, Hq * d, oq, od)
+        fa.Hip.sync()
+        outs.append((out.download(Hq * d, np.uint16), oq.download(Hq * d, np.int8),
+                     od.download(Hq * d // 32, np.float32)))
+    (o1, q1, d1), (o2, q2, d2) = outs
+    assert np.array_equal(o1, o2), "attention output"
+    assert np.array_equal(q1, q2), "int8 codes"
+    assert np.array_equal(d1.view(np.uint32), d2.view(np.uint32)), "scales"
+    oq_ref, od_ref = oracle.quantize_q8_rows(o1[None])
+    assert np.array_equal(q1, oq_ref[0]) and np.array_equal(d1.view(np.uint32), od_ref[0].view(np.uint32))
