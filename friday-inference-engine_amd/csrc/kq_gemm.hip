@@ -8,10 +8,13 @@
 // exact fp32 form; activations as q times their scale rounded to fp16) and a single fp16
 // MFMA chain with fp32 accumulation runs over K.
 //
-// Tiling: a workgroup of 256 threads owns 128 weight rows x 128 tokens; its four waves
-// each own 64 x 64 (2 x 2 tiles of v_mfma_f32_32x32x16_f16). K advances in stages of 64
-// values through two LDS buffers: while the MFMAs consume one, the raw bytes of the next
-// stage are decoded into the other and those of the stage after it are in flight.
+// Tiling: a workgroup owns BN weight rows x BT tokens (256 x 128, 128 x 128 or 64 x 64,
+// chosen by how well the grid fills the chip); its waves own 32 x 32 tiles of
+// v_mfma_f32_32x32x16_f16 (2 x 2 of them, or one). K advances in stages of 64 values
+// through two LDS buffers: while the MFMAs consume one, the raw bytes of the next stage are
+// decoded into the other and those of the stage after it are in flight.
+//
+// Also here: the decode GEMV with int8 activations (gemvQ8), on the same block decoders.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -33,11 +36,6 @@ __device__ __forceinline__ float half_bits(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
-// 4 bytes from a 2-byte aligned address (Q3_K, Q6_K and Q8_0 blocks are 2-byte aligned)
-__device__ __forceinline__ uint32_t ld16x2(const uint8_t* p) {
-    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
-    return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
-}
 __device__ __forceinline__ uint32_t ld16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
 // N 4-byte words from a 2-byte aligned address p, with aligned dword loads: from p itself
