@@ -128,4 +128,26 @@ __device__ __forceinline__ T ld_nt(const T* p) {
     return __builtin_nontemporal_load(p);
 }
 
+// Dequantize 16 int8 values with one fp16 scale into two 16-byte fp16 chunks. Each code
+// q becomes the fp16 number 1664 + q by splicing (q ^ 0x80) under the exponent byte
+// 0x66 (v_perm), minus 1664 (exact), times the scale: one fp16 rounding of the exact
+// product, the same bits as rounding the fp32 product q * scale to fp16.
+__device__ __forceinline__ void dequant16(u4 raw, float sc, u4& lo, u4& hi) {
+    const h2 s2 = h2{(_Float16)sc, (_Float16)sc};  // sc is an fp16 value: exact
+    const h2 bias = h2{(_Float16)1664.0f, (_Float16)1664.0f};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u = raw[i] ^ 0x80808080u;
+        const uint32_t d0 = __builtin_amdgcn_perm(0x66666666u, u, 0x04010400u);  // bytes u0 66 u1 66
+        const uint32_t d1 = __builtin_amdgcn_perm(0x66666666u, u, 0x04030402u);  // bytes u2 66 u3 66
+        const h2 x0 = (__builtin_bit_cast(h2, d0) - bias) * s2;
+        const h2 x1 = (__builtin_bit_cast(h2, d1) - bias) * s2;
+        o[2 * i] = __builtin_bit_cast(uint32_t, x0);
+        o[2 * i + 1] = __builtin_bit_cast(uint32_t, x1);
+    }
+    lo = u4{o[0], o[1], o[2], o[3]};
+    hi = u4{o[4], o[5], o[6], o[7]};
+}
+
 }  // namespace fa

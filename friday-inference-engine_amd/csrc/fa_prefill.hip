@@ -279,6 +279,26 @@ struct P2Geo {
     static constexpr int KSTEPS = D / 32;
     static constexpr int DTILES = D / 16;
     static constexpr int OROW = D + 4;                 // combine row stride (floats)
+    static constexpr int CREG_BYTES = 4 * (2 * kP2Slices * 16 + kP2Slices * 16 * OROW);  // one group's merge area
+};
+
+// int8 caches: raw stage = the codes of K and V (row-major, kP2KS rows of D bytes each)
+// followed by their fp16 scales (D/32 per row), copied by DMA as they lie in memory.
+template <int D>
+struct P2RawGeo {
+    static constexpr int ROWB = D;                     // code bytes of one row
+    static constexpr int CPR = ROWB / 16;              // 16-byte chunks per row
+    static constexpr int RPI = 64 / CPR;               // rows per wave DMA instruction
+    static constexpr int PART = kP2KS * ROWB;          // codes of K (or V) in a stage
+    static constexpr int SROWB = D / 16;               // scale bytes of one row
+    static constexpr int SDW = SROWB / 4;              // scale dwords of one row
+    static constexpr int SPART = kP2KS * SROWB;        // scales of K (or V) in a stage
+    static constexpr int NI = kP2KS / RPI / kP2DmaWaves;  // code DMA instructions per wave per tensor
+    static constexpr int SI = SPART / 4 / 64;          // scale DMA instructions per tensor (one per wave)
+    static constexpr int RAW = 2 * PART + 2 * SPART;
+    static constexpr int NCH = 2 * kP2KS * CPR;        // 16-code chunks of a stage (K and V)
+    static_assert(SI >= 1 && SI <= kP2DmaWaves && SPART % 256 == 0, "scale copy shape");
+    static_assert(NCH % kP2Threads == 0, "decode shape");
 };
 
 // One wave-wide global -> LDS copy (global_load_lds_dwordx4): lane l moves 16 bytes
@@ -292,15 +312,35 @@ __device__ __forceinline__ void dma16(const char* base, uint32_t off, lds_u8* ld
                  : "memory");
 }
 
-template <int D, int RA, int RB>
+// The same copy for 4 bytes per lane (global_load_lds_dword): lane l's dword lands at lds + 4*l.
+__device__ __forceinline__ void dma4(const char* base, uint32_t off, lds_u8* lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off), "s"(base)
+                 : "memory");
+}
+
+// Bytes of the LDS buffers: fp16 caches use two fp16 stages (stage0, stage1); int8
+// caches use one fp16 stage (stage0, decoded from the raw stage in use) and two raw
+// stages (stage1, stage2), the first also holding group 1's merge area.
+template <int D, bool Q8>
+struct P2Lds {
+    static constexpr int B0 = P2Geo<D>::STAGE;
+    static constexpr int RAWB = P2RawGeo<D>::RAW > P2Geo<D>::CREG_BYTES ? P2RawGeo<D>::RAW : P2Geo<D>::CREG_BYTES;
+    static constexpr int B1 = Q8 ? RAWB : P2Geo<D>::STAGE;
+    static constexpr int B2 = Q8 ? RAWB : 16;
+};
+
+template <int D, int RA, int RB, bool Q8>
 __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParams p) {
     using Gm = P2Geo<D>;
+    using Rg = P2RawGeo<D>;
+    using Lb = P2Lds<D, Q8>;
     constexpr int RT = RA;  // state arrays per lane (group 1 uses the first RB entries)
     static_assert(RB <= RA, "group 0 holds the larger share");
-    // two distinct stage buffers (not one array indexed by the tile's parity): the compiler
+    // distinct stage buffers (not one array indexed by the tile's parity): the compiler
     // then sees that the DMA into one stage does not alias the LDS reads of the other
-    __shared__ __align__(16) unsigned char stage0[Gm::STAGE];
-    __shared__ __align__(16) unsigned char stage1[Gm::STAGE];
+    __shared__ __align__(16) unsigned char stage0[Lb::B0];
+    __shared__ __align__(16) unsigned char stage1[Lb::B1];
+    __shared__ __align__(16) unsigned char stage2[Lb::B2];
 
     // grid x = kv head, y = row block (heaviest first): consecutive workgroup ids walk the
     // kv heads, so with round-robin placement over the XCDs one kv head's blocks share an
@@ -349,19 +389,30 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     const int grp_lo = row0 < R ? p0 + row0 / p.G : INT_MAX;
 
     // DMA of one stage: wave w moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K and V parts
-    const size_t rowb = (size_t)p.Hkv * Gm::ROWB;
-    const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * Gm::ROWB;
-    const char* vbase = static_cast<const char*>(p.v) + (size_t)kvh * Gm::ROWB;
-    const int drow = lane / Gm::CPR, dslot = lane % Gm::CPR;
-    // this lane's byte offsets (row, swizzled chunk) within a stage, one per DMA instruction
-    uint32_t doff[Gm::NI];
+    constexpr int CROWB = Q8 ? Rg::ROWB : Gm::ROWB;  // cache bytes of one kv-head row
+    constexpr int CCPR = Q8 ? Rg::CPR : Gm::CPR;
+    constexpr int CRPI = Q8 ? Rg::RPI : Gm::RPI;
+    constexpr int CNI = Q8 ? Rg::NI : Gm::NI;
+    const size_t rowb = (size_t)p.Hkv * CROWB;
+    const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * CROWB;
+    const char* vbase = static_cast<const char*>(p.v) + (size_t)kvh * CROWB;
+    const int drow = lane / CCPR, dslot = lane % CCPR;
+    // this lane's byte offsets (row, chunk) within a stage, one per DMA instruction; fp16
+    // rows land with their chunks swizzled, int8 rows as they are (the decode pass swizzles)
+    uint32_t doff[CNI];
 #pragma unroll
-    for (int i = 0; i < Gm::NI; ++i) {
-        const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
-        doff[i] = (uint32_t)(r * (int)rowb + (dslot ^ (r % Gm::CPR)) * 16);
+    for (int i = 0; i < CNI; ++i) {
+        const int r = (wave * CNI + i) * CRPI + drow;
+        doff[i] = (uint32_t)(r * (int)rowb + (Q8 ? dslot : (dslot ^ (r % CCPR))) * 16);
     }
-    lds_u8* const lds0 = (lds_u8*)stage0;
-    lds_u8* const lds1 = (lds_u8*)stage1;
+    lds_u8* const lds0 = (lds_u8*)(Q8 ? stage1 : stage0);
+    lds_u8* const lds1 = (lds_u8*)(Q8 ? stage2 : stage1);
+    // int8 scales: the row's D/32 fp16 scales are contiguous ([pos][kv_dim/32] layout)
+    const size_t srowb = (size_t)p.Hkv * Rg::SROWB;
+    const char* ksbase = reinterpret_cast<const char*>(p.k_scale) + (size_t)kvh * Rg::SROWB;
+    const char* vsbase = reinterpret_cast<const char*>(p.v_scale) + (size_t)kvh * Rg::SROWB;
+    const int srow = (wave * 64 + lane) / Rg::SDW;  // scale row of this lane's dword (waves < SI)
+    const uint32_t soff = (uint32_t)(srow * (int)srowb + ((wave * 64 + lane) % Rg::SDW) * 4);
     auto issue = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
         if (wave >= kP2DmaWaves) return;
         lds_u8* st = decltype(stage_tag)::value ? lds1 : lds0;
@@ -370,22 +421,53 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         const char* kt = kbase + tile0;
         const char* vt = vbase + tile0;
         const int rmax = kend - 1 - tile * kP2KS;  // rows past it re-read the last key
+        constexpr int VOFF = Q8 ? Rg::PART : Gm::STAGE_K;  // V part of the stage
         if (rmax >= kP2KS - 1) {
 #pragma unroll
-            for (int i = 0; i < Gm::NI; ++i) {
-                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
+            for (int i = 0; i < CNI; ++i) {
+                lds_u8* l = st + (wave * CNI + i) * CRPI * CROWB;
                 dma16(kt, doff[i], l);
-                dma16(vt, doff[i], l + Gm::STAGE_K);
+                dma16(vt, doff[i], l + VOFF);
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < Gm::NI; ++i) {
-                const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
-                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (dslot ^ (r % Gm::CPR)) * 16);
-                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
+            for (int i = 0; i < CNI; ++i) {
+                const int r = (wave * CNI + i) * CRPI + drow;
+                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (Q8 ? dslot : (dslot ^ (r % CCPR))) * 16);
+                lds_u8* l = st + (wave * CNI + i) * CRPI * CROWB;
                 dma16(kt, off, l);
-                dma16(vt, off, l + Gm::STAGE_K);
+                dma16(vt, off, l + VOFF);
             }
+        }
+        if constexpr (Q8) {
+            if (wave < Rg::SI) {
+                const size_t stile0 = (size_t)tile * kP2KS * srowb;
+                const uint32_t off = rmax >= kP2KS - 1
+                                         ? soff
+                                         : (uint32_t)(min(srow, rmax) * (int)srowb + ((wave * 64 + lane) % Rg::SDW) * 4);
+                lds_u8* l = st + 2 * Rg::PART + wave * 256;
+                dma4(ksbase + stile0, off, l);
+                dma4(vsbase + stile0, off, l + Rg::SPART);
+            }
+        }
+    };
+    // int8: the raw stage -> fp16 stage0 (same layout as the fp16 DMA: chunk slot
+    // chunk ^ (row % CPR)); each 16-code chunk becomes two fp16 chunks (dequant16)
+    auto decode = [&](const unsigned char* raw) __attribute__((always_inline)) {
+#pragma unroll 1  // one chunk's registers at a time: the row tiles' state is live here
+        for (int it = 0; it < Rg::NCH / kP2Threads; ++it) {
+            const int idx = it * kP2Threads + tid;
+            const int ts = idx / (kP2KS * Rg::CPR);  // 0: K, 1: V
+            const int rem = idx % (kP2KS * Rg::CPR);
+            const int r = rem / Rg::CPR, c = rem % Rg::CPR;
+            const u4 q = *reinterpret_cast<const u4*>(raw + ts * Rg::PART + rem * 16);
+            const float sc = (float)*reinterpret_cast<const _Float16*>(raw + 2 * Rg::PART + ts * Rg::SPART +
+                                                                        r * Rg::SROWB + (c >> 1) * 2);
+            u4 lo, hi;
+            dequant16(q, sc, lo, hi);
+            unsigned char* row = stage0 + ts * Gm::STAGE_K + r * Gm::ROWB;
+            *reinterpret_cast<u4*>(row + (((2 * c) ^ (r % Gm::CPR)) * 16)) = lo;
+            *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ (r % Gm::CPR)) * 16)) = hi;
         }
     };
 
@@ -519,10 +601,15 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         // wave's part of the stage has landed and every wave is done with the other stage
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        const unsigned char* sk = decltype(stage_tag)::value ? stage1 : stage0;
+        const unsigned char* sk = Q8 ? stage0 : (decltype(stage_tag)::value ? stage1 : stage0);
         const unsigned char* sv = sk + Gm::STAGE_K;
         // the next stage's DMA into the other buffer, in flight during this stage's compute
         if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
+        if constexpr (Q8) {
+            // every wave is done with the previous stage's fp16 tile (first barrier)
+            decode(decltype(stage_tag)::value ? stage2 : stage1);
+            __syncthreads();
+        }
         const int kpos0 = tile * kP2KS + wrow;  // this wave's first key position
         if (RA == RB || grp == 0)
             compute(std::integral_constant<int, RA>{}, sk, sv, kpos0);
@@ -541,8 +628,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     __syncthreads();  // every wave is done reading the stages
     // ---- merge the key slices' states, one row tile per group at a time through LDS ----
     // group g uses stage buffer g: m [slices][16], l [slices][16], O [slices][16][OROW]
-    constexpr int CREG = (2 * kP2Slices * 16 + kP2Slices * 16 * Gm::OROW);  // floats per group
-    static_assert(CREG * 4 <= Gm::STAGE, "combine fits");
+    static_assert(Gm::CREG_BYTES <= Lb::B0 && Gm::CREG_BYTES <= Lb::B1, "combine fits");
     float* cm = reinterpret_cast<float*>(grp ? stage1 : stage0);
     float* cl = cm + kP2Slices * 16;
     float* co = cl + kP2Slices * 16;
@@ -588,19 +674,19 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     }
 }
 
-template <int D, int RA, int RB>
+template <int D, int RA, int RB, bool Q8>
 int launch_dma(const PrefillParams& p, hipStream_t stream) {
     const int R = p.T * p.G;
     constexpr int rows = (RA + RB) * 16;
     const dim3 grid(p.Hkv, (R + rows - 1) / rows);
-    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RA, RB>), grid, dim3(kP2Threads), 0, stream, p);
+    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RA, RB, Q8>), grid, dim3(kP2Threads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // Row tiles per workgroup: about one workgroup per CU of the MI355X (256) for the
 // whole launch; group 0 takes ceil(RT/2) of them, group 1 the rest, at most three per
 // wave so that the registers of two waves per SIMD hold them.
-template <int D>
+template <int D, bool Q8>
 int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     static const int forced = [] {
         const char* e = std::getenv("FRIDAY_ATTN_PREFILL_RT");
@@ -611,11 +697,11 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     const int rt_max = 6;
     rt = rt < 1 ? 1 : (rt > rt_max ? rt_max : rt);
     switch (rt) {
-        case 1: return launch_dma<D, 1, 0>(p, stream);
-        case 2: return launch_dma<D, 1, 1>(p, stream);
-        case 3: return launch_dma<D, 2, 1>(p, stream);
-        case 4: return launch_dma<D, 2, 2>(p, stream);
-        default: return launch_dma<D, 3, 3>(p, stream);  // 5 as well: (3,2) spills
+        case 1: return launch_dma<D, 1, 0, Q8>(p, stream);
+        case 2: return launch_dma<D, 1, 1, Q8>(p, stream);
+        case 3: return launch_dma<D, 2, 1, Q8>(p, stream);
+        case 4: return launch_dma<D, 2, 2, Q8>(p, stream);
+        default: return launch_dma<D, 3, 3, Q8>(p, stream);  // 5 as well: (3,2) spills
     }
 }
 
@@ -630,8 +716,15 @@ int launch_pf(const PrefillParams& p, hipStream_t stream) {
 }  // namespace
 
 int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t stream) {
-    if (head_dim == 128) return q8 ? launch_pf<128, true>(p, stream) : launch_dma_rt<128>(p, stream);
-    if (head_dim == 64) return q8 ? launch_pf<64, true>(p, stream) : launch_dma_rt<64>(p, stream);
+    // the int8 DMA copies the scales by dwords: a scale array off 4-byte alignment takes
+    // the register-staged kernel
+    const bool scale_dma = ((reinterpret_cast<uintptr_t>(p.k_scale) | reinterpret_cast<uintptr_t>(p.v_scale)) & 3) == 0;
+    if (head_dim == 128)
+        return !q8 ? launch_dma_rt<128, false>(p, stream)
+                   : scale_dma ? launch_dma_rt<128, true>(p, stream) : launch_pf<128, true>(p, stream);
+    if (head_dim == 64)
+        return !q8 ? launch_dma_rt<64, false>(p, stream)
+                   : scale_dma ? launch_dma_rt<64, true>(p, stream) : launch_pf<64, true>(p, stream);
     return -2;
 }
 

@@ -52,15 +52,51 @@ def test_reference_prefill_cases(gpu, oracle, Hq, Hkv, T, p0, q8):
     assert_close(got, ref, f"prefill {Hq}/{Hkv} T={T} p0={p0} q8={q8}")
 
 
+@pytest.mark.parametrize("q8", [False, True])
 @pytest.mark.parametrize("Hq,Hkv,d,T,p0", [(14, 2, 64, 40, 0), (14, 2, 64, 129, 300), (48, 1, 128, 33, 10)])
-def test_other_shapes(gpu, oracle, Hq, Hkv, d, T, p0):
+def test_other_shapes(gpu, oracle, Hq, Hkv, d, T, p0, q8):
+    """The cache ends at p0 + T: the last stage's copies stop at its last row."""
     fa = gpu
     rng = np.random.default_rng(T * 7 + p0)
     max_ctx = p0 + T
     q = f16(rng, (T, Hq * d))
-    k, v, _, _ = make_cache(rng, max_ctx, Hkv * d, False)
-    got = run_prefill(fa, q, k, v, None, None, T, p0, Hq, Hkv, d)
-    assert_close(got, oracle.prefill(q, k, v, T, p0, Hq, Hkv, d), f"prefill {Hq}/{Hkv} d{d} T={T} p0={p0}")
+    k, v, ks, vs = make_cache(rng, max_ctx, Hkv * d, q8)
+    got = run_prefill(fa, q, k, v, ks, vs, T, p0, Hq, Hkv, d)
+    ref = oracle.prefill_q8(q, k, ks, v, vs, T, p0, Hq, Hkv, d) if q8 else oracle.prefill(q, k, v, T, p0, Hq, Hkv, d)
+    assert_close(got, ref, f"prefill {Hq}/{Hkv} d{d} T={T} p0={p0} q8={q8}")
+
+
+@pytest.mark.parametrize("p0", [0, 1024])
+def test_config4_chunk_q8(gpu, oracle, p0):
+    """Config 4 on an int8 cache: sampled rows vs the int8 decode oracle at S = p0 + t + 1."""
+    fa = gpu
+    Hq, Hkv, d, T = 40, 8, 128, 512
+    rng = np.random.default_rng(p0 + 8)
+    q = f16(rng, (T, Hq * d))
+    k, v, ks, vs = make_cache(rng, p0 + T, Hkv * d, True)
+    got = run_prefill(fa, q, k, v, ks, vs, T, p0, Hq, Hkv, d)
+    for t in sorted(set([0, 1, 127, 128, 511] + list(rng.choice(T, 5, replace=False)))):
+        ref = oracle.decode_q8(q[t], k, ks, v, vs, p0 + t + 1, Hq, Hkv, d)
+        assert_close(got[t], ref, f"config4 q8 p0={p0} t={t}")
+
+
+def test_q8_scales_off_dword_alignment(gpu, oracle):
+    """Scale arrays 2 bytes off 4-byte alignment take the register-staged kernel; same results."""
+    fa = gpu
+    Hq, Hkv, d, T, p0 = 32, 8, 128, 70, 300
+    rng = np.random.default_rng(17)
+    q = f16(rng, (T, Hq * d))
+    k, v, ks, vs = make_cache(rng, p0 + T, Hkv * d, True)
+    dq, dk, dv = (fa.DeviceBuffer.from_array(a) for a in (q, k, v))
+    dks, dvs = fa.DeviceBuffer(ks.nbytes + 4), fa.DeviceBuffer(vs.nbytes + 4)
+    dks.upload(ks, offset=2)
+    dvs.upload(vs, offset=2)
+    out = fa.DeviceBuffer(q.nbytes)
+    dpos = fa.DeviceBuffer.from_array(np.array([p0], np.int32))
+    fa.launchPrefillAttention(dq, dk, dv, out, T, dpos, Hq, Hkv, d, k_scale=dks.ptr + 2, v_scale=dvs.ptr + 2)
+    fa.Hip.sync()
+    got = as_f32(out.download((T, Hq * d), np.uint16))
+    assert_close(got, oracle.prefill_q8(q, k, ks, v, vs, T, p0, Hq, Hkv, d), "prefill q8 misaligned scales")
 
 
 @pytest.mark.parametrize("p0", [0, 1024, 7680])
