@@ -454,20 +454,37 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     // int8: the raw stage -> fp16 stage0 (same layout as the fp16 DMA: chunk slot
     // chunk ^ (row % CPR)); each 16-code chunk becomes two fp16 chunks (dequant16)
     auto decode = [&](const unsigned char* raw) __attribute__((always_inline)) {
-#pragma unroll 1  // one chunk's registers at a time: the row tiles' state is live here
-        for (int it = 0; it < Rg::NCH / kP2Threads; ++it) {
-            const int idx = it * kP2Threads + tid;
-            const int ts = idx / (kP2KS * Rg::CPR);  // 0: K, 1: V
-            const int rem = idx % (kP2KS * Rg::CPR);
-            const int r = rem / Rg::CPR, c = rem % Rg::CPR;
-            const u4 q = *reinterpret_cast<const u4*>(raw + ts * Rg::PART + rem * 16);
-            const float sc = (float)*reinterpret_cast<const _Float16*>(raw + 2 * Rg::PART + ts * Rg::SPART +
-                                                                        r * Rg::SROWB + (c >> 1) * 2);
-            u4 lo, hi;
-            dequant16(q, sc, lo, hi);
-            unsigned char* row = stage0 + ts * Gm::STAGE_K + r * Gm::ROWB;
-            *reinterpret_cast<u4*>(row + (((2 * c) ^ (r % Gm::CPR)) * 16)) = lo;
-            *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ (r % Gm::CPR)) * 16)) = hi;
+        constexpr int NIT = Rg::NCH / kP2Threads;
+        // chunks whose LDS reads are issued together: their latencies overlap; a larger batch
+        // spills at the largest row-tile share
+        constexpr int NB = 2;
+        static_assert(NIT % NB == 0, "decode batches");
+#pragma unroll 1
+        for (int it0 = 0; it0 < NIT; it0 += NB) {
+            u4 q[NB];
+            float sc[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int idx = (it0 + b) * kP2Threads + tid;
+                const int ts = idx / (kP2KS * Rg::CPR);  // 0: K, 1: V
+                const int rem = idx % (kP2KS * Rg::CPR);
+                const int r = rem / Rg::CPR, c = rem % Rg::CPR;
+                q[b] = *reinterpret_cast<const u4*>(raw + ts * Rg::PART + rem * 16);
+                sc[b] = (float)*reinterpret_cast<const _Float16*>(raw + 2 * Rg::PART + ts * Rg::SPART +
+                                                                   r * Rg::SROWB + (c >> 1) * 2);
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int idx = (it0 + b) * kP2Threads + tid;
+                const int ts = idx / (kP2KS * Rg::CPR);
+                const int rem = idx % (kP2KS * Rg::CPR);
+                const int r = rem / Rg::CPR, c = rem % Rg::CPR;
+                u4 lo, hi;
+                dequant16(q[b], sc[b], lo, hi);
+                unsigned char* row = stage0 + ts * Gm::STAGE_K + r * Gm::ROWB;
+                *reinterpret_cast<u4*>(row + (((2 * c) ^ (r % Gm::CPR)) * 16)) = lo;
+                *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ (r % Gm::CPR)) * 16)) = hi;
+            }
         }
     };
 
