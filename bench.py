@@ -261,28 +261,38 @@ def decode_config(cx, name, S, L, Hq, Hkv, d, steps, warmup, cold):
             "kv_GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(1e3 / ms, 1)}
 
 
-def prefill_config(cx, p0, steps, warmup):
-    """512-token causal chunk after p0 cached tokens, 40q/8kv d128, MFMA."""
+def prefill_config(cx, p0, steps, warmup, q8=False):
+    """512-token causal chunk after p0 cached tokens, 40q/8kv d128, MFMA.
+    q8: int8 caches with one fp16 scale per 32 values (random codes, scales of 0.01 scale)."""
     import numpy as np
 
     fa = cx.fa
     T, Hq, Hkv, d = 512, 40, 8, 128
     S = p0 + T
-    L = max(2, -(-2 * MALL_BYTES // (2 * S * Hkv * d * 2)))  # rotate caches beyond the MALL
-    lb = S * Hkv * d * 2
+    esz = 1 if q8 else 2
+    lb = S * Hkv * d * esz
+    sb = S * Hkv * d // 32 * 2
+    L = max(2, -(-2 * MALL_BYTES // (2 * (lb + (sb if q8 else 0)))))  # rotate caches beyond the MALL
     k, v = fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * lb)
-    cx.fill(k, L * S * Hkv * d, 5)
-    cx.fill(v, L * S * Hkv * d, 6)
+    cx.fill(k, L * lb // 2, 5)  # int8: the fp16 fill's bytes serve as codes
+    cx.fill(v, L * lb // 2, 6)
+    ks = vs = None
+    if q8:
+        ks, vs = fa.DeviceBuffer(L * sb), fa.DeviceBuffer(L * sb)
+        cx.fill(ks, L * sb // 2, 8, scale=0.01)
+        cx.fill(vs, L * sb // 2, 9, scale=0.01)
     q, out = fa.DeviceBuffer(T * Hq * d * 2), fa.DeviceBuffer(T * Hq * d * 2)
     cx.fill(q, T * Hq * d, 7)
     pos = fa.DeviceBuffer.from_array(np.array([p0], np.int32))
     ms = cx.timed(lambda: [fa.launchPrefillAttention(q, k.ptr + l * lb, v.ptr + l * lb, out, T, pos, Hq, Hkv, d,
-                                                     cx.stream.s) for l in range(L)], steps, warmup) / L
-    for b in (k, v, q, out, pos):
+                                                     cx.stream.s, k_scale=ks.ptr + l * sb if q8 else None,
+                                                     v_scale=vs.ptr + l * sb if q8 else None)
+                                   for l in range(L)], steps, warmup) / L
+    for b in (k, v, q, out, pos) + ((ks, vs) if q8 else ()):
         b.free()
     flops = 4.0 * d * Hq * (T * p0 + T * (T + 1) / 2)  # causal (unmasked) QK^T and PV flops
     tf = flops / (ms * 1e-3) / 1e12
-    return {"config": "4: chunked prefill", "T": T, "p0": p0, "heads": f"{Hq}q/{Hkv}kv d{d}",
+    return {"config": "4: chunked prefill" + (" (int8 KV)" if q8 else ""), "T": T, "p0": p0, "heads": f"{Hq}q/{Hkv}kv d{d}",
             "us_per_chunk": round(ms * 1e3, 2), "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
             "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "tokens_per_s": round(T / (ms * 1e-3), 0)}
 
@@ -526,6 +536,8 @@ def main():
                                    False))
         for p0 in (0, 1024, 2048, 4096, 7680):
             lines.append(prefill_config(cx, p0, args.steps, args.warmup))
+        for p0 in (0, 7680):
+            lines.append(prefill_config(cx, p0, args.steps, args.warmup, q8=True))
         lines.append(paged_config(cx, args.steps, args.warmup))
         lines.append(q8_config(cx, 32768, 64, args.steps, args.warmup))
         for case in GEMM_CASES:
@@ -543,6 +555,8 @@ def main():
     if args.config == "prefill":
         for p0 in (0, 1024, 2048, 4096, 7680):
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup)), flush=True)
+        for p0 in (0, 2048, 7680):
+            print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup, q8=True)), flush=True)
     if args.config == "layer":
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True)), flush=True)
