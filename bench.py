@@ -323,6 +323,7 @@ def gemm_config(cx, kind, K, N, what, steps, warmup):
     xq, xd = fa.DeviceBuffer(T * K), fa.DeviceBuffer.from_array(np.full((T, K // 32), 0.01, np.float32))
     cx.fill(xq, T * K // 2, 13)
     Y = fa.DeviceBuffer(T * N * 2)
+    fa.gemmQ8Reserve(T, K, N, cx.stream.s)  # K-split workspace, sized before capture (engine init)
     ms = cx.timed(lambda: fa.gemmQ8(kind, dW, xq, xd, T, K, N, Y, N, cx.stream.s), steps, warmup)
     for b in (dW, xq, xd, Y):
         b.free()

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -455,6 +456,64 @@ int friday_quantize_q8_rows(const uint16_t* x, int rows, int K, int8_t* xq, floa
 
 int friday_gemm_q8_supported(int kind, int K) { return kq_kind_ok(kind) && K > 0 && K % 256 == 0 ? 1 : 0; }
 
+namespace {
+// K-split workspaces of friday_gemm_q8, one per (device, stream): launches on one stream
+// run in order, so they can share it. A workspace grows only outside stream capture; the
+// buffers it outgrows stay allocated until the process ends, because a captured graph
+// may still hold them.
+struct GemmWs {
+    int dev;
+    void* stream;
+    void* ptr;
+    size_t bytes;
+};
+std::mutex g_ws_mu;
+std::vector<GemmWs> g_ws;
+std::vector<void*> g_ws_retired;
+
+// The workspace of (current device, stream) with at least `bytes`, or null when that would
+// need an allocation during stream capture. Sets *rc on a HIP error.
+void* gemm_workspace(void* stream, size_t bytes, int* rc) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return *rc = -1, nullptr;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    GemmWs* e = nullptr;
+    for (auto& w : g_ws)
+        if (w.dev == dev && w.stream == stream) e = &w;
+    if (e && e->bytes >= bytes) return e->ptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs) != hipSuccess) (void)hipGetLastError();
+    if (cs != hipStreamCaptureStatusNone) return nullptr;
+    const size_t nb = ((bytes + (1u << 20) - 1) >> 20) << 20;
+    void* ptr = nullptr;
+    if (hipMalloc(&ptr, nb) != hipSuccess) return *rc = -1, nullptr;
+    // counters start at zero; ordered before the launch that follows on this stream
+    if (hipMemsetAsync(ptr, 0, (size_t)fa::kKqMaxCounters * fa::kCounterStride * 4, static_cast<hipStream_t>(stream)) !=
+        hipSuccess)
+        return *rc = -1, nullptr;
+    if (e) {
+        g_ws_retired.push_back(e->ptr);
+        e->ptr = ptr;
+        e->bytes = nb;
+    } else {
+        g_ws.push_back(GemmWs{dev, stream, ptr, nb});
+    }
+    return ptr;
+}
+}  // namespace
+
+int friday_gemm_q8_reserve(int T, int K, int N, void* stream) {
+    const char* w = "gemm_q8_reserve";
+    if (T <= 0 || N <= 0 || K <= 0 || K % 256) return fail(FA_ERR_INVALID, "%s: invalid T=%d K=%d N=%d", w, T, K, N);
+    const fa::KqSplit sp = fa::kq_gemm_split(T, K, N);
+    if (sp.ksplit <= 1) return ok();
+    int rc = 0;
+    if (!gemm_workspace(stream, sp.bytes, &rc))
+        return fail(rc ? FA_ERR_LAUNCH : FA_ERR_WORKSPACE, "%s: %s", w,
+                    rc ? "workspace allocation failed" : "cannot allocate during stream capture");
+    return ok();
+}
+
 int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
                    int ldy, void* stream, const float* bias, const uint16_t* res) {
     const char* w = "gemm_q8";
@@ -472,6 +531,17 @@ int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, i
     p.W = static_cast<const uint8_t*>(W); p.xq = xq; p.xd = xd; p.Y = Y; p.bias = bias; p.res = res;
     p.row_bytes = friday_q8_row_bytes(kind, K);
     p.T = T; p.K = K; p.N = N; p.ldy = ldy;
+    const fa::KqSplit sp = fa::kq_gemm_split(T, K, N);
+    if (sp.ksplit > 1) {
+        int rc = 0;
+        char* ws = static_cast<char*>(gemm_workspace(stream, sp.bytes, &rc));
+        if (rc) return fail(FA_ERR_LAUNCH, "%s: split workspace allocation failed", w);
+        if (ws) {  // else (stream capture without a reserved workspace): one pass over K
+            p.ksplit = sp.ksplit; p.sps = sp.sps;
+            p.counters = reinterpret_cast<int*>(ws);
+            p.part = reinterpret_cast<float*>(ws + sp.counter_bytes);
+        }
+    }
     return launch_status(fa::launch_kq_gemm(kind, p, static_cast<hipStream_t>(stream)), w);
 }
 

@@ -131,7 +131,22 @@ struct KqGemmParams {
     const uint16_t* res;   // same layout as Y, or null (may alias Y)
     size_t row_bytes;
     int T, K, N, ldy;
+    // K split (ksplit > 1): split z takes the 64-value stages [z sps, (z + 1) sps); the
+    // workspace holds per-tile arrival counters (zero between launches) and fp32 partials
+    int ksplit = 1, sps = 0;
+    int* counters = nullptr;
+    float* part = nullptr;
 };
+// The split workspace starts with a fixed region of kKqMaxCounters counters (kCounterStride
+// ints apart), so that launches of any shape can share one workspace: each launch leaves
+// the counters it used at zero.
+constexpr int kKqMaxCounters = 4096;
+struct KqSplit {
+    int ksplit, sps;
+    size_t counter_bytes;  // workspace: the counter region, then the partials
+    size_t bytes;          // whole workspace (0 when ksplit = 1)
+};
+KqSplit kq_gemm_split(int T, int K, int N);
 int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream);
 struct KqGemvParams {
     const uint8_t* W;      // [N][row_bytes]

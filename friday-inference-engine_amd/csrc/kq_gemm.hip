@@ -317,6 +317,11 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
     // XCD and its L2 copy of the weight rows
     const int nrb = (p.N + BN - 1) / BN, ntb = (p.T + BT - 1) / BT;
     const int id = blockIdx.x;
+    // K split z = blockIdx.y covers the stages [sbeg, sbeg + nst) (all of K when ksplit = 1)
+    const int z = blockIdx.y;
+    const int sps = p.ksplit > 1 ? p.sps : p.K / kGBK;
+    const int sbeg = z * sps;
+    const int nst = min(p.K / kGBK - sbeg, sps);
     const int rb = (id % 8) + 8 * (id / (8 * ntb));
     const int tb = (id / 8) % ntb;
     if (rb >= nrb) return;  // padding of the last group of 8 row blocks
@@ -401,21 +406,64 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
 
     // stage st: loads of st + 2 into the set that held st, MFMAs on LDS buffer st % 2,
     // decode of st + 1 (loaded one stage earlier) into the other buffer, barrier
-    const int nst = p.K / kGBK;
-    load_stage(raw0, 0);
-    if (nst > 1) load_stage(raw1, 1);
-    store_stage(raw0, 0, sw0, sx0);
+    // (st counts from the split's first stage)
+    load_stage(raw0, sbeg);
+    if (nst > 1) load_stage(raw1, sbeg + 1);
+    store_stage(raw0, sbeg, sw0, sx0);
     __syncthreads();
     for (int st = 0; st < nst; st += 2) {
-        if (st + 2 < nst) load_stage(raw0, st + 2);
+        if (st + 2 < nst) load_stage(raw0, sbeg + st + 2);
         compute(sw0, sx0);
-        if (st + 1 < nst) store_stage(raw1, st + 1, sw1, sx1);
+        if (st + 1 < nst) store_stage(raw1, sbeg + st + 1, sw1, sx1);
         __syncthreads();
         if (st + 1 >= nst) break;
-        if (st + 3 < nst) load_stage(raw1, st + 3);
+        if (st + 3 < nst) load_stage(raw1, sbeg + st + 3);
         compute(sw1, sx1);
-        if (st + 2 < nst) store_stage(raw0, st + 2, sw0, sx0);
+        if (st + 2 < nst) store_stage(raw0, sbeg + st + 2, sw0, sx0);
         __syncthreads();
+    }
+
+    // K split: every split writes its accumulators as fp32 partials, float4 v of thread tid
+    // at float4 index ((z * gridDim.x + id) * NV + v) * NT + tid, written through to the
+    // device coherence point; the last of the tile's splits to arrive adds them in split
+    // order (the same bits whichever split arrives last), applies the epilogue and re-arms
+    // the tile's counter
+    if (p.ksplit > 1) {
+        constexpr int NV = TN * TT * 4;
+        const __amdgpu_buffer_rsrc_t rp = coherent_rsrc(p.part, 0x7fffffff);
+        auto off = [&](int zz, int v) { return (uint32_t)((((size_t)zz * gridDim.x + id) * NV + v) * NT + tid) * 16u; };
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    st_coherent4(rp, off(z, (i * TT + j) * 4 + q),
+                                 f4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+        __shared__ int s_last;
+        wait_vmem();
+        __syncthreads();
+        if (tid == 0) {
+            int* cnt = p.counters + (size_t)id * kCounterStride;
+            const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = prev == p.ksplit - 1;
+            if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!s_last) return;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int v = (i * TT + j) * 4 + q;
+                    const f4 mine = f4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    f4 tot = z == 0 ? mine : ld_coherent4(rp, off(0, v));
+                    for (int zz = 1; zz < p.ksplit; ++zz) tot += zz == z ? mine : ld_coherent4(rp, off(zz, v));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = tot[e];
+                }
     }
 
     // acc[i][j][r]: weight row n0 + (wn TN + i) 32 + 8(r/4) + 4(lane/32) + r%4,
@@ -577,7 +625,7 @@ template <int WVN, int WVT, int TN, int TT>
 int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
     constexpr int BN = 32 * WVN * TN, BT = 32 * WVT * TT;
     const int nrb = (p.N + BN - 1) / BN, ntb = (p.T + BT - 1) / BT;
-    const dim3 grid(((nrb + 7) / 8) * 8 * ntb), block(64 * WVN * WVT);
+    const dim3 grid(((nrb + 7) / 8) * 8 * ntb, p.ksplit), block(64 * WVN * WVT);
     switch (kind) {
         case kKqQ2K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ2K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
         case kKqQ3K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ3K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
@@ -596,11 +644,46 @@ int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
 // CUs, else 128 x 128 (four waves, two per CU) when it gives at least 1.5 workgroups per
 // CU, else 64 x 64 (four waves, one tile each) so that small-N / large-K shapes still
 // spread over the chip. FRIDAY_GEMM_TILE = 1 / 2 / 3 forces one of them.
+// K split for shapes that fill neither tile: 128 x 128 tiles with the split count (2 to 8,
+// at least 16 stages of 64 K values each) that best fills 512 workgroup slots (two per
+// CU), the smaller count on ties. FRIDAY_GEMM_KSPLIT = 1 turns it off, n > 1 forces n.
+KqSplit kq_gemm_split(int T, int K, int N) {
+    static const int forced = [] {
+        const char* e = std::getenv("FRIDAY_GEMM_KSPLIT");
+        return e && *e ? std::atoi(e) : 0;
+    }();
+    KqSplit r{1, K / kGBK, 0, 0};
+    auto wgs = [&](int bn, int bt) { return (long)((N + bn - 1) / bn) * ((T + bt - 1) / bt); };
+    const int nst = K / kGBK;
+    const long tiles = wgs(128, 128);
+    int best = 1;
+    if (forced > 1) {
+        best = forced;
+    } else if (forced == 0 && wgs(256, 128) < 256 && tiles < 384) {
+        double fill_best = 0.0;
+        for (int sk = 2; sk <= 8 && nst / sk >= 16; ++sk) {
+            const long n = tiles * sk;
+            const double fill = (double)n / (512.0 * ((n + 511) / 512));
+            if (fill > fill_best + 1e-9) fill_best = fill, best = sk;
+        }
+    }
+    if (best <= 1 || nst < 2) return r;
+    r.sps = (nst + best - 1) / best;
+    r.ksplit = (nst + r.sps - 1) / r.sps;
+    const long gx = ((N + 127) / 128 + 7) / 8 * 8 * ((T + 127) / 128);  // grid x of the 128 x 128 launch
+    if (r.ksplit <= 1 || gx > kKqMaxCounters) return KqSplit{1, nst, 0, 0};
+    r.counter_bytes = (size_t)kKqMaxCounters * kCounterStride * 4;
+    r.bytes = r.counter_bytes + (size_t)r.ksplit * gx * 256 * 64 * 4;   // 256 threads x 64 accumulators
+    if (r.bytes >= ((size_t)1 << 31)) return KqSplit{1, nst, 0, 0};      // 32-bit buffer offsets
+    return r;
+}
+
 int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
     static const int forced = [] {
         const char* e = std::getenv("FRIDAY_GEMM_TILE");
         return e && *e ? std::atoi(e) : 0;
     }();
+    if (p.ksplit > 1) return launch_kq_shape<2, 2, 2, 2>(kind, p, stream);
     auto wgs = [&](int bn, int bt) { return (long)((p.N + bn - 1) / bn) * ((p.T + bt - 1) / bt); };
     int shape = forced;
     if (shape < 1 || shape > 4) shape = wgs(256, 128) >= 256 ? 1 : (wgs(128, 128) >= 384 ? 2 : 3);

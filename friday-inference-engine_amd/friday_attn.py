@@ -62,6 +62,7 @@ API = [
     ("friday_quantize_q8_rows", _I, [_P, _I, _I, _P, _P, _P]),
     ("friday_gemm_q8_supported", _I, [_I, _I]),
     ("friday_gemm_q8", _I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _P]),
+    ("friday_gemm_q8_reserve", _I, [_I, _I, _I, _P]),
     ("friday_gemv_q8", _I, [_I, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
 ]
 
@@ -415,6 +416,11 @@ def gemmQ8Supported(kind, K) -> bool:
 def gemmQ8(kind, W, xq, xd, T, K, N, Y, ldy, stream=None, bias=None, res=None):
     _check(load().friday_gemm_q8(kind, _ptr(W), _ptr(xq), _ptr(xd), T, K, N, _ptr(Y), ldy, stream, _ptr(bias),
                                  _ptr(res)))
+
+
+def gemmQ8Reserve(T, K, N, stream=None):
+    """Size the K-split workspace of gemmQ8 for (T, K, N) on `stream` before stream capture."""
+    _check(load().friday_gemm_q8_reserve(T, K, N, stream))
 
 
 def gemvQ8(kind, W, xq, xd, K, N, y, stream=None, W2=None, y2=None, bias=None, res=None):

@@ -158,3 +158,83 @@ def test_gemv_two_matrices_bias(gpu, oracle):
     f = lambda a: a.view(np.float16).astype(np.float32)  # noqa: E731
     assert_gemm_close(f(y), f(r1[0]), "y")
     assert_gemm_close(f(y2), f(r2[0]), "y2")
+
+
+# ---- K split (shapes whose 128 x 128 tiles do not fill the GPU): fp32 partials in the
+# library's per-stream workspace, summed in split order by the last workgroup of a tile.
+
+SPLIT_SHAPES = [(256, 4096, 512, 3), (200, 2048, 384, 5), (512, 3072, 256, 6)]
+
+
+@pytest.mark.parametrize("T,K,N,kind", SPLIT_SHAPES)
+def test_split_k_all_rows(gpu, oracle, T, K, N, kind):
+    """Every output against the oracle, with bias and the residual in place."""
+    fa = gpu
+    rng = np.random.default_rng(T + K + N)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    res = rng.standard_normal((T, N), dtype=np.float32).astype(np.float16).view(np.uint16)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    Y, xq, xd = run_gemm(fa, kind, W, x, T, K, N, bias=bias, res=True, y_init=res)
+    ref, _ = oracle.gemm_q8(kind, W, xq, xd, T, K, N, bias=bias, res=res)
+    assert_gemm_close(Y.view(np.float16).astype(np.float32), ref.view(np.float16).astype(np.float32),
+                      f"split {KQ_KINDS[kind][0]} T={T} K={K} N={N}")
+
+
+def test_split_k_repeatable(gpu):
+    """The tile counters re-arm: repeated calls, with a call of another split shape on the
+    same stream in between, give identical bits."""
+    fa = gpu
+    rng = np.random.default_rng(5)
+    kind, T, K, N = 3, 256, 4096, 512
+    W = fa.DeviceBuffer.from_array(kq_random_weights(rng, kind, N, K))
+    W2 = fa.DeviceBuffer.from_array(kq_random_weights(rng, kind, 256, 8192))
+    dq, dd = fa.DeviceBuffer(T * 8192), fa.DeviceBuffer(T * 8192 // 32 * 4)
+    x = rng.standard_normal((T, 8192), dtype=np.float32).astype(np.float16).view(np.uint16)
+    fa.quantizeQ8Rows(fa.DeviceBuffer.from_array(x), T, 8192, dq, dd)
+    dY, dY2 = fa.DeviceBuffer(T * N * 2), fa.DeviceBuffer(T * 256 * 2)
+    outs = []
+    for i in range(3):
+        fa.gemmQ8(kind, W, dq, dd, T, K, N, dY, N)  # rows of xq read with stride K
+        if i == 1:
+            fa.gemmQ8(kind, W2, dq, dd, T, 8192, 256, dY2, 256)
+        fa.Hip.sync()
+        outs.append(dY.download((T, N), np.uint16))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_split_k_graph_replay(gpu, oracle):
+    """gemmQ8Reserve before capture: the captured split GEMM replays bit-identically to the
+    eager call; a stream with no workspace captures the unsplit GEMM, which also matches
+    the oracle."""
+    fa = gpu
+    rng = np.random.default_rng(6)
+    kind, T, K, N = 5, 256, 4096, 512
+    Wh = kq_random_weights(rng, kind, N, K)
+    W = fa.DeviceBuffer.from_array(Wh)
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    dq, dd = fa.DeviceBuffer(T * K), fa.DeviceBuffer(T * K // 32 * 4)
+    fa.quantizeQ8Rows(fa.DeviceBuffer.from_array(x), T, K, dq, dd)
+    fa.Hip.sync()
+    eager = fa.DeviceBuffer(T * N * 2)
+    fa.gemmQ8(kind, W, dq, dd, T, K, N, eager, N)
+    fa.Hip.sync()
+    ref_bits = eager.download((T, N), np.uint16)
+    xq, xd = dq.download((T, K), np.int8), dd.download((T, K // 32), np.float32)
+    ref, _ = oracle.gemm_q8(kind, Wh, xq, xd, T, K, N)
+    for reserve in (True, False):
+        stream = fa.Stream()
+        if reserve:
+            fa.gemmQ8Reserve(T, K, N, stream.s)
+            stream.synchronize()
+        dY = fa.DeviceBuffer(T * N * 2)
+        graph = fa.Graph(stream, lambda: fa.gemmQ8(kind, W, dq, dd, T, K, N, dY, N, stream=stream.s))
+        for _ in range(3):
+            dY.fill_bytes(0)
+            graph.launch()
+            stream.synchronize()
+            got = dY.download((T, N), np.uint16)
+            if reserve:
+                assert np.array_equal(got, ref_bits), "captured split GEMM differs from eager"
+            assert_gemm_close(got.view(np.float16).astype(np.float32), ref.view(np.float16).astype(np.float32),
+                              f"graph reserve={reserve}")
