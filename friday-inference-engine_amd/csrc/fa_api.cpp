@@ -505,8 +505,7 @@ void* gemm_workspace(void* stream, size_t bytes, int* rc) {
 int friday_gemm_q8_reserve(int T, int K, int N, void* stream) {
     const char* w = "gemm_q8_reserve";
     if (T <= 0 || N <= 0 || K <= 0 || K % 256) return fail(FA_ERR_INVALID, "%s: invalid T=%d K=%d N=%d", w, T, K, N);
-    const fa::KqSplit sp = fa::kq_gemm_split(T, K, N);
-    if (sp.ksplit <= 1) return ok();
+    const fa::KqPlan sp = fa::kq_gemm_plan(T, K, N);
     int rc = 0;
     if (!gemm_workspace(stream, sp.bytes, &rc))
         return fail(rc ? FA_ERR_LAUNCH : FA_ERR_WORKSPACE, "%s: %s", w,
@@ -531,15 +530,18 @@ int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, i
     p.W = static_cast<const uint8_t*>(W); p.xq = xq; p.xd = xd; p.Y = Y; p.bias = bias; p.res = res;
     p.row_bytes = friday_q8_row_bytes(kind, K);
     p.T = T; p.K = K; p.N = N; p.ldy = ldy;
-    const fa::KqSplit sp = fa::kq_gemm_split(T, K, N);
-    if (sp.ksplit > 1) {
-        int rc = 0;
-        char* ws = static_cast<char*>(gemm_workspace(stream, sp.bytes, &rc));
-        if (rc) return fail(FA_ERR_LAUNCH, "%s: split workspace allocation failed", w);
-        if (ws) {  // else (stream capture without a reserved workspace): one pass over K
+    const fa::KqPlan sp = fa::kq_gemm_plan(T, K, N);
+    int rc = 0;
+    char* ws = static_cast<char*>(gemm_workspace(stream, sp.bytes, &rc));
+    if (rc) return fail(FA_ERR_LAUNCH, "%s: workspace allocation failed", w);
+    // no workspace (stream capture without friday_gemm_q8_reserve): one pass over K, and each
+    // workgroup dequantises its activation tile itself (the same values)
+    if (ws) {
+        p.xh = reinterpret_cast<const uint16_t*>(ws + sp.xh_off);
+        if (sp.ksplit > 1) {
             p.ksplit = sp.ksplit; p.sps = sp.sps;
             p.counters = reinterpret_cast<int*>(ws);
-            p.part = reinterpret_cast<float*>(ws + sp.counter_bytes);
+            p.part = reinterpret_cast<float*>(ws + sp.part_off);
         }
     }
     return launch_status(fa::launch_kq_gemm(kind, p, static_cast<hipStream_t>(stream)), w);

@@ -136,17 +136,21 @@ struct KqGemmParams {
     int ksplit = 1, sps = 0;
     int* counters = nullptr;
     float* part = nullptr;
+    // optional [T][K] fp16 buffer: the launch first dequantises xq / xd into it once, and
+    // the GEMM stages fp16 activations from it (null: each workgroup dequantises its tile)
+    const uint16_t* xh = nullptr;
 };
-// The split workspace starts with a fixed region of kKqMaxCounters counters (kCounterStride
-// ints apart), so that launches of any shape can share one workspace: each launch leaves
-// the counters it used at zero.
+// GEMM workspace: a fixed region of kKqMaxCounters split counters (kCounterStride ints
+// apart; each launch leaves the counters it used at zero, so launches of any shape can
+// share one workspace), the fp16 activations [T][K], then the split partials.
 constexpr int kKqMaxCounters = 4096;
-struct KqSplit {
+struct KqPlan {
     int ksplit, sps;
-    size_t counter_bytes;  // workspace: the counter region, then the partials
-    size_t bytes;          // whole workspace (0 when ksplit = 1)
+    size_t xh_off;         // byte offset of the fp16 activations
+    size_t part_off;       // byte offset of the partials (ksplit > 1)
+    size_t bytes;          // whole workspace
 };
-KqSplit kq_gemm_split(int T, int K, int N);
+KqPlan kq_gemm_plan(int T, int K, int N);
 int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream);
 struct KqGemvParams {
     const uint8_t* W;      // [N][row_bytes]

@@ -29,6 +29,15 @@ namespace {
 constexpr int kGBK = 64;  // K values per stage (two 32-value blocks)
 constexpr int kGRowB = kGBK * 2;  // bytes of one fp16 tile row in LDS
 
+// One wave-wide global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane l
+// moves base + off to lds + 16 l (base and lds wave-uniform). Issued from inline assembly,
+// so that the compiler does not drain it before unrelated LDS accesses.
+typedef __attribute__((address_space(3))) unsigned char gm_lds_u8;
+__device__ __forceinline__ void gm_dma16(const void* base, uint32_t off, gm_lds_u8* lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off), "s"(base)
+                 : "memory");
+}
+
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
@@ -302,7 +311,7 @@ __device__ __forceinline__ uint16_t epilogue(float acc, const float* bias, const
 // so BN = 32 WVN TN weight rows and BT = 32 WVT TT tokens per workgroup. Staging: thread
 // u < 2 BN decodes half u % 2 (32 values) of weight row u / 2 of each stage, thread
 // u >= NT - 2 BT the same for token row (u - (NT - 2 BT)) / 2.
-template <int KIND, int WVN, int WVT, int TN, int TT>
+template <int KIND, int WVN, int WVT, int TN, int TT, bool XH>
 __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p) {
     constexpr int NT = 64 * WVN * WVT;
     constexpr int BN = 32 * WVN * TN, BT = 32 * WVT * TT;
@@ -341,6 +350,22 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
     const uint8_t* wrow = p.W + (size_t)(w_ok ? n0 + wr_ : 0) * row_bytes;
     const int8_t* xrow = p.xq + (size_t)(x_ok ? t0 + xr_ : 0) * p.K;
     const float* xdrow = p.xd + (size_t)(x_ok ? t0 + xr_ : 0) * (p.K / 32);
+    // XH: the activations were dequantised to fp16 once for the whole call (dequant_x_kernel,
+    // the same bits as store_x32). The x-role waves copy a stage's tile straight into LDS
+    // (gm_dma16), 8 tile rows per instruction: lane l fills row 8i + l/8, slot l%8, i.e.
+    // chunk (l%8) ^ ((row >> 1) & 7) of the row (tile_off's swizzle); rows past T re-read
+    // row T - 1 (their outputs are not stored).
+    constexpr int XWAVES = 2 * BT / 64;           // x-role waves
+    constexpr int XNI = BT / 8 / XWAVES;          // copies per x-role wave and stage
+    static_assert(XNI * XWAVES * 8 == BT, "x copy shape");
+    const int xw = wave - (NT - 2 * BT) / 64;     // index among the x-role waves
+    uint32_t xoff[XNI];
+#pragma unroll
+    for (int i = 0; i < XNI; ++i) {
+        const int r = (xw * XNI + i) * 8 + (lane >> 3);
+        const int t = min(t0 + r, p.T - 1);
+        xoff[i] = (uint32_t)(((size_t)t * p.K + (((lane & 7) ^ ((r >> 1) & 7)) * 8)) * 2);
+    }
     const bool w_wave = __builtin_amdgcn_readfirstlane(w_role);
     const bool x_wave = __builtin_amdgcn_readfirstlane(x_role);
 
@@ -352,10 +377,25 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
         float xs;
     };
     Raw raw0, raw1;
+    // XH copy of stage st into the tile sx. Issued before the weight loads of stage st + 1
+    // (in program order), so it is older than them: the compiler's wait for those registers,
+    // before they are decoded into LDS ahead of the barrier that publishes stage st, leaves
+    // only younger loads outstanding (loads complete in order), i.e. this copy has landed.
+    // Waves without a weight role wait explicitly (wait_x below).
+    auto load_xh = [&](int st, unsigned char* sx) __attribute__((always_inline)) {
+        if (x_wave) {
+            const uint16_t* base = p.xh + (size_t)st * kGBK;
+#pragma unroll
+            for (int i = 0; i < XNI; ++i) gm_dma16(base, xoff[i], (gm_lds_u8*)(sx + (xw * XNI + i) * 8 * kGRowB));
+        }
+    };
+    auto wait_x = [&]() __attribute__((always_inline)) {
+        if (XH && !w_wave) wait_vmem();
+    };
     auto load_stage = [&](Raw& r, int st) __attribute__((always_inline)) {
         const int blk = st * (kGBK / 32) + lh;
         if (w_wave) load_wraw<KIND>(wrow, blk, r.w);
-        if (x_wave) {
+        if (!XH && x_wave) {
             r.xa = *reinterpret_cast<const uint4*>(xrow + 32 * blk);
             r.xb = *reinterpret_cast<const uint4*>(xrow + 32 * blk + 16);
             r.xs = xdrow[blk];
@@ -370,7 +410,7 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
             }
             store_w32(sw, wr_, lh, wb.u, wb.ws, wb.c);
         }
-        if (x_wave) store_x32(sx, xr_, lh, r.xa, r.xb, x_ok ? r.xs : 0.0f);
+        if (!XH && x_wave) store_x32(sx, xr_, lh, r.xa, r.xb, x_ok ? r.xs : 0.0f);
     };
 
     f16v acc[TN][TT];
@@ -407,19 +447,27 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
     // stage st: loads of st + 2 into the set that held st, MFMAs on LDS buffer st % 2,
     // decode of st + 1 (loaded one stage earlier) into the other buffer, barrier
     // (st counts from the split's first stage)
+    // (XH: the activation copy of stage st + 1 is issued at the top of stage st, before the
+    // weight loads of stage st + 2, into the buffer that stage st - 1 used)
+    if (XH) load_xh(sbeg, sx0);
     load_stage(raw0, sbeg);
     if (nst > 1) load_stage(raw1, sbeg + 1);
     store_stage(raw0, sbeg, sw0, sx0);
+    wait_x();
     __syncthreads();
     for (int st = 0; st < nst; st += 2) {
+        if (XH && st + 1 < nst) load_xh(sbeg + st + 1, sx1);
         if (st + 2 < nst) load_stage(raw0, sbeg + st + 2);
         compute(sw0, sx0);
         if (st + 1 < nst) store_stage(raw1, sbeg + st + 1, sw1, sx1);
+        wait_x();
         __syncthreads();
         if (st + 1 >= nst) break;
+        if (XH && st + 2 < nst) load_xh(sbeg + st + 2, sx0);
         if (st + 3 < nst) load_stage(raw1, sbeg + st + 3);
         compute(sw1, sx1);
         if (st + 2 < nst) store_stage(raw0, sbeg + st + 2, sw0, sx0);
+        wait_x();
         __syncthreads();
     }
 
@@ -621,21 +669,58 @@ __global__ __launch_bounds__(256) void quantize_q8_rows_kernel(const uint16_t* _
     if ((idx & 31) == 0) xd[row * (K / 32) + blk] = d;
 }
 
-template <int WVN, int WVT, int TN, int TT>
-int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
+// xq [n] int8 with xd [n / 32] -> xh [n] fp16, each value exactly as store_x32 forms it
+// (fp16(1664 + q) - 1664, times fp16(xd), in packed fp16); 16 values per thread.
+__global__ __launch_bounds__(256) void dequant_x_kernel(const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                        size_t n16, uint16_t* __restrict__ xh) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n16) return;
+    const uint4 q = reinterpret_cast<const uint4*>(xq)[i];
+    const float d = xd[i >> 1];
+    const h2v s2 = h2v{(_Float16)d, (_Float16)d};
+    const h2v bias = h2v{(_Float16)1664.0f, (_Float16)1664.0f};
+    const uint32_t in[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t u = in[k] ^ 0x80808080u;
+        const uint32_t d0 = __builtin_amdgcn_perm(0x66666666u, u, 0x04010400u);
+        const uint32_t d1 = __builtin_amdgcn_perm(0x66666666u, u, 0x04030402u);
+        o[2 * k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2v, d0) - bias) * s2);
+        o[2 * k + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2v, d1) - bias) * s2);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(xh) + 2 * i;
+    dst[0] = uint4{o[0], o[1], o[2], o[3]};
+    dst[1] = uint4{o[4], o[5], o[6], o[7]};
+}
+
+template <int WVN, int WVT, int TN, int TT, bool XH>
+int launch_kq_shape_x(int kind, const KqGemmParams& p, hipStream_t stream) {
     constexpr int BN = 32 * WVN * TN, BT = 32 * WVT * TT;
     const int nrb = (p.N + BN - 1) / BN, ntb = (p.T + BT - 1) / BT;
     const dim3 grid(((nrb + 7) / 8) * 8 * ntb, p.ksplit), block(64 * WVN * WVT);
     switch (kind) {
-        case kKqQ2K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ2K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
-        case kKqQ3K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ3K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
-        case kKqQ4K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ4K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
-        case kKqQ5K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ5K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
-        case kKqQ6K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ6K, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
-        case kKqQ80: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ80, WVN, WVT, TN, TT>), grid, block, 0, stream, p); break;
+        case kKqQ2K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ2K, WVN, WVT, TN, TT, XH>), grid, block, 0, stream, p); break;
+        case kKqQ3K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ3K, WVN, WVT, TN, TT, XH>), grid, block, 0, stream, p); break;
+        case kKqQ4K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ4K, WVN, WVT, TN, TT, XH>), grid, block, 0, stream, p); break;
+        case kKqQ5K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ5K, WVN, WVT, TN, TT, XH>), grid, block, 0, stream, p); break;
+        case kKqQ6K: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ6K, WVN, WVT, TN, TT, XH>), grid, block, 0, stream, p); break;
+        case kKqQ80: hipLaunchKernelGGL((kq_gemm_kernel<kKqQ80, WVN, WVT, TN, TT, XH>), grid, block, 0, stream, p); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int WVN, int WVT, int TN, int TT>
+int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
+    if (p.xh) {
+        const size_t n16 = (size_t)p.T * p.K / 16;
+        hipLaunchKernelGGL(dequant_x_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, stream, p.xq, p.xd, n16,
+                           const_cast<uint16_t*>(p.xh));
+        if (hipGetLastError() != hipSuccess) return -1;
+        return launch_kq_shape_x<WVN, WVT, TN, TT, true>(kind, p, stream);
+    }
+    return launch_kq_shape_x<WVN, WVT, TN, TT, false>(kind, p, stream);
 }
 
 }  // namespace
@@ -647,12 +732,14 @@ int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
 // K split for shapes that fill neither tile: 128 x 128 tiles with the split count (2 to 8,
 // at least 16 stages of 64 K values each) that best fills 512 workgroup slots (two per
 // CU), the smaller count on ties. FRIDAY_GEMM_KSPLIT = 1 turns it off, n > 1 forces n.
-KqSplit kq_gemm_split(int T, int K, int N) {
+KqPlan kq_gemm_plan(int T, int K, int N) {
     static const int forced = [] {
         const char* e = std::getenv("FRIDAY_GEMM_KSPLIT");
         return e && *e ? std::atoi(e) : 0;
     }();
-    KqSplit r{1, K / kGBK, 0, 0};
+    const size_t cbytes = (size_t)kKqMaxCounters * kCounterStride * 4;
+    const size_t xbytes = (((size_t)T * K * 2 + 255) / 256) * 256;
+    KqPlan r{1, K / kGBK, cbytes, cbytes + xbytes, cbytes + xbytes};
     auto wgs = [&](int bn, int bt) { return (long)((N + bn - 1) / bn) * ((T + bt - 1) / bt); };
     const int nst = K / kGBK;
     const long tiles = wgs(128, 128);
@@ -668,13 +755,14 @@ KqSplit kq_gemm_split(int T, int K, int N) {
         }
     }
     if (best <= 1 || nst < 2) return r;
-    r.sps = (nst + best - 1) / best;
-    r.ksplit = (nst + r.sps - 1) / r.sps;
+    const int sps = (nst + best - 1) / best;
+    const int ks = (nst + sps - 1) / sps;
     const long gx = ((N + 127) / 128 + 7) / 8 * 8 * ((T + 127) / 128);  // grid x of the 128 x 128 launch
-    if (r.ksplit <= 1 || gx > kKqMaxCounters) return KqSplit{1, nst, 0, 0};
-    r.counter_bytes = (size_t)kKqMaxCounters * kCounterStride * 4;
-    r.bytes = r.counter_bytes + (size_t)r.ksplit * gx * 256 * 64 * 4;   // 256 threads x 64 accumulators
-    if (r.bytes >= ((size_t)1 << 31)) return KqSplit{1, nst, 0, 0};      // 32-bit buffer offsets
+    const size_t pbytes = (size_t)ks * gx * 256 * 64 * 4;               // 256 threads x 64 accumulators
+    if (ks <= 1 || gx > kKqMaxCounters || pbytes >= ((size_t)1 << 31)) return r;  // 32-bit buffer offsets
+    r.ksplit = ks;
+    r.sps = sps;
+    r.bytes = r.part_off + pbytes;
     return r;
 }
 

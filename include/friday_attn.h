@@ -224,16 +224,17 @@ int friday_gemm_q8_supported(int kind, int K);
  * W must be 4-byte aligned, xq 16-byte aligned, ldy >= N. Runs on gfx950 fp16 MFMA over
  * operands decoded in LDS; agrees with the reference's integer form within its own GEMM
  * test bar (test_prefill_gemm.cu:111-129: rel-L2 < 1e-3, max |diff| < 1e-2 RMS).
- * Shapes whose output tiles do not fill the GPU (e.g. T = 512 with N = 4096, K = 14336)
- * split K over workgroups: fp32 partials in a library-held workspace, one per (device,
- * stream), allocated on first use (as the reference's module scratch, hpc_k_quants.cu:
- * 869-880) and summed in a fixed order, so results do not depend on timing. Under stream
- * capture the workspace is not allocated: a call then runs unsplit unless
- * friday_gemm_q8_reserve sized it beforehand. */
+ * A library-held workspace, one per (device, stream), allocated on first use (as the
+ * reference's module scratch, hpc_k_quants.cu:869-880), holds the activations dequantised
+ * to fp16 once per call and, for shapes whose output tiles do not fill the GPU (e.g.
+ * T = 512 with N = 4096, K = 14336), the fp32 partials of a K split, summed in a fixed
+ * order so that results do not depend on timing. Under stream capture the workspace is not
+ * allocated: a call then dequantises per workgroup and runs unsplit (same values, slower)
+ * unless friday_gemm_q8_reserve sized it beforehand. */
 int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
                    int ldy, void* stream, const float* bias, const uint16_t* res);
 /* No counterpart in the reference (its GEMM needs no workspace; cf. ensureQ8Scratch,
- * hpc_k_quants.h:52): sizes the K-split workspace of friday_gemm_q8 for (T, K, N) on
+ * hpc_k_quants.h:52): sizes the workspace of friday_gemm_q8 for (T, K, N) on
  * `stream` ahead of stream capture. FA_ERR_WORKSPACE when called during capture and an
  * allocation would be needed. */
 int friday_gemm_q8_reserve(int T, int K, int N, void* stream);

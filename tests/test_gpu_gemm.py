@@ -238,3 +238,26 @@ def test_split_k_graph_replay(gpu, oracle):
                 assert np.array_equal(got, ref_bits), "captured split GEMM differs from eager"
             assert_gemm_close(got.view(np.float16).astype(np.float32), ref.view(np.float16).astype(np.float32),
                               f"graph reserve={reserve}")
+
+
+@pytest.mark.parametrize("T,K,N,kind", [(130, 768, 96, 4), (37, 1024, 200, 1), (300, 1024, 2100, 6)])
+def test_prehoisted_activations_bit_identical(gpu, T, K, N, kind):
+    """The eager call dequantises the activations once into the workspace (fp16) and stages
+    them from there; a call captured on a stream with no workspace dequantises them in every
+    workgroup. Same values, same accumulation order (shapes with too few stages to split
+    K): the outputs agree bit for bit."""
+    fa = gpu
+    rng = np.random.default_rng(T * N)
+    W = fa.DeviceBuffer.from_array(kq_random_weights(rng, kind, N, K))
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    dq, dd = fa.DeviceBuffer(T * K), fa.DeviceBuffer(T * K // 32 * 4)
+    fa.quantizeQ8Rows(fa.DeviceBuffer.from_array(x), T, K, dq, dd)
+    eager = fa.DeviceBuffer(T * N * 2)
+    fa.gemmQ8(kind, W, dq, dd, T, K, N, eager, N)
+    fa.Hip.sync()
+    stream = fa.Stream()  # fresh stream: no workspace, and none is allocated under capture
+    dY = fa.DeviceBuffer(T * N * 2)
+    graph = fa.Graph(stream, lambda: fa.gemmQ8(kind, W, dq, dd, T, K, N, dY, N, stream=stream.s))
+    graph.launch()
+    stream.synchronize()
+    assert np.array_equal(dY.download((T, N), np.uint16), eager.download((T, N), np.uint16))
