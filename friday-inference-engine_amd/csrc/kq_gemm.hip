@@ -17,6 +17,7 @@
 // Also here: the decode GEMV with int8 activations (gemvQ8), on the same block decoders.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 
@@ -580,11 +581,12 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
     if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
 }
 
-// LDS-staged decode GEMV: a workgroup takes 4 consecutive weight rows (contiguous bytes),
-// copies them into LDS with one burst of global_load_lds_dword (every copy in flight at
-// once, no registers), then each wave computes its row as kq_gemv_kernel does, reading the
-// blocks from LDS. Rows start in LDS at the same offsets mod 4 as in memory, so the
-// 2-byte aligned kinds use the same realigning loads.
+// LDS-staged decode GEMV: a workgroup of ROWS waves takes ROWS consecutive weight rows
+// (contiguous bytes) and copies them into LDS in one burst of global->LDS copies (every copy
+// in flight at once, no registers), optionally followed by the activations (XL); then each
+// wave computes its row as kq_gemv_kernel does, reading the blocks from LDS. Rows start in
+// LDS at the same offsets mod 4 as in memory, so the 2-byte aligned kinds use the same
+// realigning loads.
 typedef __attribute__((address_space(3))) unsigned char gv_lds_u8;
 __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, gv_lds_u8* lds) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off),
@@ -592,12 +594,12 @@ __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, gv_lds_u
                  : "memory");
 }
 
-template <int KIND>
-__global__ __launch_bounds__(256) void kq_gemv_lds_kernel(KqGemvParams p) {
+template <int KIND, int ROWS, bool XL>
+__global__ __launch_bounds__(64 * ROWS) void kq_gemv_lds_kernel(KqGemvParams p) {
     extern __shared__ __align__(16) unsigned char rows_lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int gpm = (p.N + 3) / 4;  // row groups per matrix
+    const int gpm = (p.N + ROWS - 1) / ROWS;  // row groups per matrix
     int g = blockIdx.x;
     const uint8_t* W = p.W;
     uint16_t* y = p.y;
@@ -606,30 +608,51 @@ __global__ __launch_bounds__(256) void kq_gemv_lds_kernel(KqGemvParams p) {
         W = p.W2;
         y = p.y2;
     }
-    const int n0 = g * 4;
-    const int nrows = min(4, p.N - n0);
-    const uint32_t span = (uint32_t)(nrows * p.row_bytes);  // a multiple of 4 bytes (4 rows or up to the end)
-    const uint8_t* src = W + (size_t)n0 * p.row_bytes;      // 4-byte aligned: n0 is a multiple of 4
+    const int n0 = g * ROWS;
+    const int nrows = min(ROWS, p.N - n0);
+    // a multiple of 4 bytes: the launcher takes this kernel only when every group's rows are
+    const uint32_t span = (uint32_t)(nrows * p.row_bytes);
+    const uint8_t* src = W + (size_t)n0 * p.row_bytes;  // 4-byte aligned: W is, n0 is even, row_bytes even
     gv_lds_u8* lds = (gv_lds_u8*)rows_lds;
-    // wave w copies 256-byte pieces w, w + 4, ...; lane l moves bytes 4l..4l+3 of a piece
-    const uint32_t pieces = (span + 255) / 256;
-    for (uint32_t i = wave; i < pieces; i += 4) {
-        const uint32_t off = min(256 * i + 4 * lane, span - 4);  // the tail re-reads the last word
-        dma4(src, off, lds + 256 * i);
+    // from a 16-byte aligned start, whole 1 KiB pieces by global_load_lds_dwordx4 (lane l moves
+    // bytes 16l..16l+15; wave w takes pieces w, w + ROWS, ...); the rest (or everything, from
+    // a start off 16-byte alignment) in 256-byte pieces of global_load_lds_dword, lane l moving
+    // bytes 4l..4l+3, the tail re-reading the last word
+    const uint32_t big = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? span / 1024 : 0;
+    for (uint32_t i = wave; i < big; i += ROWS) gm_dma16(src, 1024 * i + 16 * lane, lds + 1024 * i);
+    const uint32_t rest0 = 1024 * big;
+    const uint32_t pieces = (span - rest0 + 255) / 256;
+    for (uint32_t i = wave; i < pieces; i += ROWS) {
+        const uint32_t off = min(rest0 + 256 * i + 4 * lane, span - 4);
+        dma4(src, off, lds + rest0 + 256 * i);
+    }
+    // XL: the activations (xq: K bytes, 16-byte aligned; xd: K / 8 bytes) after the rows, at
+    // xoff = ROWS row_bytes rounded up to 256
+    const uint32_t xoff = ((ROWS * (uint32_t)p.row_bytes + 255) / 256) * 256;
+    if constexpr (XL) {
+        const uint32_t xb = (uint32_t)p.K, db = (uint32_t)p.K / 8, r0 = xb / 1024 * 1024;
+        for (uint32_t i = wave; i < xb / 1024; i += ROWS)
+            gm_dma16(reinterpret_cast<const char*>(p.xq), 1024 * i + 16 * lane, lds + xoff + 1024 * i);
+        for (uint32_t i = wave; i < (xb - r0 + 255) / 256; i += ROWS)
+            dma4(reinterpret_cast<const uint8_t*>(p.xq), min(r0 + 256 * i + 4 * lane, xb - 4), lds + xoff + r0 + 256 * i);
+        for (uint32_t i = wave; i < (db + 255) / 256; i += ROWS)
+            dma4(reinterpret_cast<const uint8_t*>(p.xd), min(256 * i + 4 * lane, db - 4), lds + xoff + xb + 256 * i);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (wave >= nrows) return;
     const int row = n0 + wave;
     const unsigned char* wrow = rows_lds + (size_t)wave * p.row_bytes;
+    const int8_t* xq = XL ? reinterpret_cast<const int8_t*>(rows_lds + xoff) : p.xq;
+    const float* xd = XL ? reinterpret_cast<const float*>(rows_lds + xoff + p.K) : p.xd;
     const int nblk = p.K / 32;
     float acc = 0.0f;
     for (int blk = lane; blk < nblk; blk += 64) {
         WRaw r;
         load_wraw<KIND>(wrow, blk, r);
-        const uint4 xa = *reinterpret_cast<const uint4*>(p.xq + 32 * blk);
-        const uint4 xb = *reinterpret_cast<const uint4*>(p.xq + 32 * blk + 16);
-        const float dx = p.xd[blk];
+        const uint4 xa = *reinterpret_cast<const uint4*>(xq + 32 * blk);
+        const uint4 xb = *reinterpret_cast<const uint4*>(xq + 32 * blk + 16);
+        const float dx = xd[blk];
         WBlock b;
         decode_wraw<KIND>(r, blk, b);
         const int x[8] = {(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w, (int)xb.x, (int)xb.y, (int)xb.z, (int)xb.w};
@@ -781,27 +804,55 @@ int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
     return launch_kq_shape<2, 2, 1, 1>(kind, p, stream);
 }
 
-// The LDS-staged GEMV when four rows fit in 64 KiB (two workgroups per CU), else one wave
-// per row straight from memory. FRIDAY_GEMV_LDS = 0 forces the direct kernel.
+template <int ROWS, bool XL>
+int launch_gemv_lds(int kind, const KqGemvParams& p, size_t lds, hipStream_t stream) {
+    const dim3 grid(((p.N + ROWS - 1) / ROWS) * (p.W2 ? 2 : 1)), block(64 * ROWS);
+    switch (kind) {
+        case kKqQ2K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ2K, ROWS, XL>), grid, block, lds, stream, p); break;
+        case kKqQ3K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ3K, ROWS, XL>), grid, block, lds, stream, p); break;
+        case kKqQ4K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ4K, ROWS, XL>), grid, block, lds, stream, p); break;
+        case kKqQ5K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ5K, ROWS, XL>), grid, block, lds, stream, p); break;
+        case kKqQ6K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ6K, ROWS, XL>), grid, block, lds, stream, p); break;
+        case kKqQ80: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ80, ROWS, XL>), grid, block, lds, stream, p); break;
+        default: return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// The LDS-staged GEMV when its rows (and activations) fit in 64 KiB (two or more workgroups
+// per CU) and every row group spans a multiple of 4 bytes, else one wave per row straight
+// from memory. FRIDAY_GEMV_LDS = 0 forces the direct kernel; FRIDAY_GEMV_ROWS (2 / 4 / 8)
+// and FRIDAY_GEMV_XL (0 / 1) override the rows per workgroup and the activation staging.
 int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream) {
-    static const bool lds_ok = [] {
+    static const int env_lds = [] {
         const char* e = std::getenv("FRIDAY_GEMV_LDS");
-        return !(e && *e == '0');
+        return e && *e ? std::atoi(e) : 1;
+    }();
+    static const int env_rows = [] {
+        const char* e = std::getenv("FRIDAY_GEMV_ROWS");
+        return e && *e ? std::atoi(e) : 0;
+    }();
+    static const int env_xl = [] {
+        const char* e = std::getenv("FRIDAY_GEMV_XL");
+        return e && *e ? std::atoi(e) : -1;
     }();
     const int rows = p.W2 ? 2 * p.N : p.N;
-    const size_t lds = ((4 * p.row_bytes + 255) / 256) * 256;
-    if (lds_ok && lds <= 65536) {
-        const dim3 grid(((p.N + 3) / 4) * (p.W2 ? 2 : 1)), block(256);
-        switch (kind) {
-            case kKqQ2K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ2K>, grid, block, lds, stream, p); break;
-            case kKqQ3K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ3K>, grid, block, lds, stream, p); break;
-            case kKqQ4K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ4K>, grid, block, lds, stream, p); break;
-            case kKqQ5K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ5K>, grid, block, lds, stream, p); break;
-            case kKqQ6K: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ6K>, grid, block, lds, stream, p); break;
-            case kKqQ80: hipLaunchKernelGGL(kq_gemv_lds_kernel<kKqQ80>, grid, block, lds, stream, p); break;
-            default: return -2;
-        }
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+    int nr = env_rows == 2 || env_rows == 4 || env_rows == 8 ? env_rows : 4;
+    const bool span4 = p.row_bytes % 4 == 0 || p.N % 2 == 0;
+    const size_t xbytes = (((size_t)p.K + p.K / 8 + 255) / 256) * 256;
+    auto rows_bytes = [&](int r) { return ((r * p.row_bytes + 255) / 256) * 256; };
+    while (nr > 2 && rows_bytes(nr) > 65536) nr /= 2;
+    // activations in LDS when that keeps the workgroups per CU (160 KiB of LDS, at most 32
+    // waves): measured 5 % faster at 32B attn_output, 3 % slower at 8B ffn_down where it
+    // would cost a workgroup per CU
+    auto per_cu = [&](size_t b) { return std::min<size_t>(32 / nr, 163840 / b); };
+    bool xl = per_cu(rows_bytes(nr) + xbytes) >= per_cu(rows_bytes(nr)) && rows_bytes(nr) + xbytes <= 65536;
+    if (env_xl >= 0) xl = env_xl != 0;
+    const size_t lds = rows_bytes(nr) + (xl ? xbytes : 0);
+    if (env_lds != 0 && span4 && lds <= 65536) {
+        if (nr == 2) return xl ? launch_gemv_lds<2, true>(kind, p, lds, stream) : launch_gemv_lds<2, false>(kind, p, lds, stream);
+        if (nr == 8) return xl ? launch_gemv_lds<8, true>(kind, p, lds, stream) : launch_gemv_lds<8, false>(kind, p, lds, stream);
+        return xl ? launch_gemv_lds<4, true>(kind, p, lds, stream) : launch_gemv_lds<4, false>(kind, p, lds, stream);
     }
     const dim3 grid((rows + 3) / 4), block(256);
     switch (kind) {

@@ -261,3 +261,18 @@ def test_prehoisted_activations_bit_identical(gpu, T, K, N, kind):
     graph.launch()
     stream.synchronize()
     assert np.array_equal(dY.download((T, N), np.uint16), eager.download((T, N), np.uint16))
+
+
+@pytest.mark.parametrize("kind,N", [(5, 63), (5, 62), (2, 61), (6, 70), (3, 65)])
+def test_gemv_row_group_tails(gpu, oracle, kind, N):
+    """Row counts that leave a short last row group; with an odd N and a 2-byte aligned kind
+    (Q3_K, Q6_K, Q8_0) the groups would not span whole words and the direct kernel runs."""
+    fa = gpu
+    K = 2048
+    rng = np.random.default_rng(kind * 100 + N)
+    W = kq_random_weights(rng, kind, N, K)
+    x = rng.standard_normal((1, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    y, _, xq, xd = run_gemv(fa, kind, W, x, K, N)
+    ref, _ = oracle.gemm_q8(kind, W, xq, xd, 1, K, N)
+    assert_gemm_close(y.view(np.float16).astype(np.float32), ref.view(np.float16).astype(np.float32),
+                      f"gemv tail {KQ_KINDS[kind][0]} N={N}")
