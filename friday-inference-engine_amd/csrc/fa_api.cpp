@@ -537,7 +537,7 @@ int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, i
     // no workspace (stream capture without friday_gemm_q8_reserve): one pass over K, and each
     // workgroup dequantises its activation tile itself (the same values)
     if (ws) {
-        p.xh = reinterpret_cast<const uint16_t*>(ws + sp.xh_off);
+        if (sp.xh) p.xh = reinterpret_cast<const uint16_t*>(ws + sp.xh_off);
         if (sp.ksplit > 1) {
             p.ksplit = sp.ksplit; p.sps = sp.sps;
             p.counters = reinterpret_cast<int*>(ws);

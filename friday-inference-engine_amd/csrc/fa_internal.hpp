@@ -146,6 +146,7 @@ struct KqGemmParams {
 constexpr int kKqMaxCounters = 4096;
 struct KqPlan {
     int ksplit, sps;
+    bool xh;               // stage fp16 activations from the workspace (T K 2 < 4 GiB: 32-bit offsets)
     size_t xh_off;         // byte offset of the fp16 activations
     size_t part_off;       // byte offset of the partials (ksplit > 1)
     size_t bytes;          // whole workspace

@@ -761,8 +761,9 @@ KqPlan kq_gemm_plan(int T, int K, int N) {
         return e && *e ? std::atoi(e) : 0;
     }();
     const size_t cbytes = (size_t)kKqMaxCounters * kCounterStride * 4;
-    const size_t xbytes = (((size_t)T * K * 2 + 255) / 256) * 256;
-    KqPlan r{1, K / kGBK, cbytes, cbytes + xbytes, cbytes + xbytes};
+    const bool xh = (size_t)T * K * 2 < ((size_t)1 << 32);  // the copies use 32-bit offsets
+    const size_t xbytes = xh ? (((size_t)T * K * 2 + 255) / 256) * 256 : 0;
+    KqPlan r{1, K / kGBK, xh, cbytes, cbytes + xbytes, cbytes + xbytes};
     auto wgs = [&](int bn, int bt) { return (long)((N + bn - 1) / bn) * ((T + bt - 1) / bt); };
     const int nst = K / kGBK;
     const long tiles = wgs(128, 128);
