@@ -34,8 +34,13 @@ constexpr int kGRowB = kGBK * 2;  // bytes of one fp16 tile row in LDS
 // moves base + off to lds + 16 l (base and lds wave-uniform). Issued from inline assembly,
 // so that the compiler does not drain it before unrelated LDS accesses.
 typedef __attribute__((address_space(3))) unsigned char gm_lds_u8;
+// The LDS address goes through readfirstlane: it is wave-uniform, but the compiler may hold
+// it in a VGPR (e.g. when derived from a boolean), which the SGPR operand cannot take.
+__device__ __forceinline__ uint32_t lds_sgpr(const void* lds) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)lds);
+}
 __device__ __forceinline__ void gm_dma16(const void* base, uint32_t off, gm_lds_u8* lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off), "s"(base)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_sgpr((const void*)lds)), "v"(off), "s"(base)
                  : "memory");
 }
 
@@ -589,63 +594,16 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
 // realigning loads.
 typedef __attribute__((address_space(3))) unsigned char gv_lds_u8;
 __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, gv_lds_u8* lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off),
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_sgpr((const void*)lds)), "v"(off),
                  "s"(base)
                  : "memory");
 }
 
-template <int KIND, int ROWS, bool XL>
-__global__ __launch_bounds__(64 * ROWS) void kq_gemv_lds_kernel(KqGemvParams p) {
-    extern __shared__ __align__(16) unsigned char rows_lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int gpm = (p.N + ROWS - 1) / ROWS;  // row groups per matrix
-    int g = blockIdx.x;
-    const uint8_t* W = p.W;
-    uint16_t* y = p.y;
-    if (g >= gpm) {
-        g -= gpm;
-        W = p.W2;
-        y = p.y2;
-    }
-    const int n0 = g * ROWS;
-    const int nrows = min(ROWS, p.N - n0);
-    // a multiple of 4 bytes: the launcher takes this kernel only when every group's rows are
-    const uint32_t span = (uint32_t)(nrows * p.row_bytes);
-    const uint8_t* src = W + (size_t)n0 * p.row_bytes;  // 4-byte aligned: W is, n0 is even, row_bytes even
-    gv_lds_u8* lds = (gv_lds_u8*)rows_lds;
-    // from a 16-byte aligned start, whole 1 KiB pieces by global_load_lds_dwordx4 (lane l moves
-    // bytes 16l..16l+15; wave w takes pieces w, w + ROWS, ...); the rest (or everything, from
-    // a start off 16-byte alignment) in 256-byte pieces of global_load_lds_dword, lane l moving
-    // bytes 4l..4l+3, the tail re-reading the last word
-    const uint32_t big = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? span / 1024 : 0;
-    for (uint32_t i = wave; i < big; i += ROWS) gm_dma16(src, 1024 * i + 16 * lane, lds + 1024 * i);
-    const uint32_t rest0 = 1024 * big;
-    const uint32_t pieces = (span - rest0 + 255) / 256;
-    for (uint32_t i = wave; i < pieces; i += ROWS) {
-        const uint32_t off = min(rest0 + 256 * i + 4 * lane, span - 4);
-        dma4(src, off, lds + rest0 + 256 * i);
-    }
-    // XL: the activations (xq: K bytes, 16-byte aligned; xd: K / 8 bytes) after the rows, at
-    // xoff = ROWS row_bytes rounded up to 256
-    const uint32_t xoff = ((ROWS * (uint32_t)p.row_bytes + 255) / 256) * 256;
-    if constexpr (XL) {
-        const uint32_t xb = (uint32_t)p.K, db = (uint32_t)p.K / 8, r0 = xb / 1024 * 1024;
-        for (uint32_t i = wave; i < xb / 1024; i += ROWS)
-            gm_dma16(reinterpret_cast<const char*>(p.xq), 1024 * i + 16 * lane, lds + xoff + 1024 * i);
-        for (uint32_t i = wave; i < (xb - r0 + 255) / 256; i += ROWS)
-            dma4(reinterpret_cast<const uint8_t*>(p.xq), min(r0 + 256 * i + 4 * lane, xb - 4), lds + xoff + r0 + 256 * i);
-        for (uint32_t i = wave; i < (db + 255) / 256; i += ROWS)
-            dma4(reinterpret_cast<const uint8_t*>(p.xd), min(256 * i + 4 * lane, db - 4), lds + xoff + xb + 256 * i);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (wave >= nrows) return;
-    const int row = n0 + wave;
-    const unsigned char* wrow = rows_lds + (size_t)wave * p.row_bytes;
-    const int8_t* xq = XL ? reinterpret_cast<const int8_t*>(rows_lds + xoff) : p.xq;
-    const float* xd = XL ? reinterpret_cast<const float*>(rows_lds + xoff + p.K) : p.xd;
-    const int nblk = p.K / 32;
+// One weight row in LDS against the activations (xq, xd; LDS or global): lane l takes
+// blocks l, l + 64, ...; returns the wave-summed fp32 dot product (every lane).
+template <int KIND>
+__device__ __forceinline__ float gemv_row(const unsigned char* wrow, const int8_t* xq, const float* xd, int nblk,
+                                          int lane) {
     float acc = 0.0f;
     for (int blk = lane; blk < nblk; blk += 64) {
         WRaw r;
@@ -669,6 +627,60 @@ __global__ __launch_bounds__(64 * ROWS) void kq_gemv_lds_kernel(KqGemvParams p) 
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    return acc;
+}
+
+// Copy `span` bytes (a multiple of 4) from src (4-byte aligned) to lds with the nw waves of
+// the workgroup: from a 16-byte aligned start, whole 1 KiB pieces by global_load_lds_dwordx4
+// (lane l moves bytes 16l..16l+15; wave w takes pieces w, w + nw, ...), the rest (or
+// everything, from a start off 16-byte alignment) in 256-byte pieces of global_load_lds_dword,
+// lane l moving bytes 4l..4l+3, the tail re-reading the last word. LDS receives up to
+// span rounded up to 256 bytes.
+__device__ __forceinline__ void copy_span(const void* src, uint32_t span, gv_lds_u8* lds, int wave, int nw, int lane) {
+    const uint32_t big = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? span / 1024 : 0;
+    for (uint32_t i = wave; i < big; i += nw) gm_dma16(src, 1024 * i + 16 * lane, lds + 1024 * i);
+    const uint32_t rest0 = 1024 * big;
+    const uint32_t pieces = (span - rest0 + 255) / 256;
+    for (uint32_t i = wave; i < pieces; i += nw)
+        dma4(static_cast<const uint8_t*>(src), min(rest0 + 256 * i + 4 * lane, span - 4), lds + rest0 + 256 * i);
+}
+
+template <int KIND, int ROWS, bool XL>
+__global__ __launch_bounds__(64 * ROWS) void kq_gemv_lds_kernel(KqGemvParams p) {
+    extern __shared__ __align__(16) unsigned char rows_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gpm = (p.N + ROWS - 1) / ROWS;  // row groups per matrix
+    int g = blockIdx.x;
+    const uint8_t* W = p.W;
+    uint16_t* y = p.y;
+    if (g >= gpm) {
+        g -= gpm;
+        W = p.W2;
+        y = p.y2;
+    }
+    const int n0 = g * ROWS;
+    const int nrows = min(ROWS, p.N - n0);
+    // a multiple of 4 bytes: the launcher takes this kernel only when every group's rows are
+    const uint32_t span = (uint32_t)(nrows * p.row_bytes);
+    const uint8_t* src = W + (size_t)n0 * p.row_bytes;  // 4-byte aligned: W is, n0 is even, row_bytes even
+    gv_lds_u8* lds = (gv_lds_u8*)rows_lds;
+    copy_span(src, span, lds, wave, ROWS, lane);
+    // XL: the activations (xq: K bytes, 16-byte aligned; xd: K / 8 bytes) after the rows, at
+    // xoff = ROWS row_bytes rounded up to 256
+    const uint32_t xoff = ((ROWS * (uint32_t)p.row_bytes + 255) / 256) * 256;
+    if constexpr (XL) {
+        copy_span(p.xq, (uint32_t)p.K, lds + xoff, wave, ROWS, lane);
+        copy_span(p.xd, (uint32_t)p.K / 8, lds + xoff + p.K, wave, ROWS, lane);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (wave >= nrows) return;
+    const int row = n0 + wave;
+    const unsigned char* wrow = rows_lds + (size_t)wave * p.row_bytes;
+    const int8_t* xq = XL ? reinterpret_cast<const int8_t*>(rows_lds + xoff) : p.xq;
+    const float* xd = XL ? reinterpret_cast<const float*>(rows_lds + xoff + p.K) : p.xd;
+    const float acc = gemv_row<KIND>(wrow, xq, xd, p.K / 32, lane);
     if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
 }
 
