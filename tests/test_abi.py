@@ -168,6 +168,10 @@ def test_gemm_q8_validation(fa):
     # row bytes of the GGML layouts
     assert [L.friday_q8_row_bytes(k, 512) for k in range(1, 7)] == [168, 220, 288, 352, 420, 544]
     assert L.friday_q8_row_bytes(fa.Q2_K, 300) == 0
+    # workspace reservation: positive T, N and K a multiple of 256 (checked before any HIP call)
+    assert L.friday_gemm_q8_reserve(0, 4096, 64, None) == fa.FA_ERR_INVALID
+    assert L.friday_gemm_q8_reserve(4, 4000, 64, None) == fa.FA_ERR_INVALID
+    assert L.friday_gemm_q8_reserve(4, 4096, -1, None) == fa.FA_ERR_INVALID
     # activation quantiser: K multiple of 32
     assert L.friday_quantize_q8_rows(FAKE, 2, 48, FAKE, FAKE, None) == fa.FA_ERR_INVALID
     assert L.friday_quantize_q8_rows(FAKE, 0, 64, FAKE, FAKE, None) == fa.FA_OK
