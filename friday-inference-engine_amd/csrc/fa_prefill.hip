@@ -612,7 +612,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         }
     };
 
-    auto step = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
+    auto step = [&](int tile, auto stage_tag, auto n_tag) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
         // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
         // wave's part of the stage has landed and every wave is done with the other stage
@@ -628,17 +628,26 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             __syncthreads();
         }
         const int kpos0 = tile * kP2KS + wrow;  // this wave's first key position
-        if (RA == RB || grp == 0)
-            compute(std::integral_constant<int, RA>{}, sk, sv, kpos0);
-        else
-            compute(std::integral_constant<int, RB>{}, sk, sv, kpos0);
+        compute(n_tag, sk, sv, kpos0);
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
+    // one copy of the stage loop per group share: the two groups run the same barriers, and
+    // each copy is register-allocated on its own (a branch per stage inside one loop keeps
+    // both shares' values live and spills when RA != RB)
+    using NA = std::integral_constant<int, RA>;
+    using NB = std::integral_constant<int, RB>;
     issue(0, S0{});
-    for (int tile = 0; tile < ntiles; tile += 2) {
-        step(tile, S0{});
-        if (tile + 1 < ntiles) step(tile + 1, S1{});
+    if (RA == RB || grp == 0) {
+        for (int tile = 0; tile < ntiles; tile += 2) {
+            step(tile, S0{}, NA{});
+            if (tile + 1 < ntiles) step(tile + 1, S1{}, NA{});
+        }
+    } else {
+        for (int tile = 0; tile < ntiles; tile += 2) {
+            step(tile, S0{}, NB{});
+            if (tile + 1 < ntiles) step(tile + 1, S1{}, NB{});
+        }
     }
 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -702,7 +711,8 @@ int launch_dma(const PrefillParams& p, hipStream_t stream) {
 
 // Row tiles per workgroup: about one workgroup per CU of the MI355X (256) for the
 // whole launch; group 0 takes ceil(RT/2) of them, group 1 the rest, at most three per
-// wave so that the registers of two waves per SIMD hold them.
+// wave so that the registers of two waves per SIMD hold them (RT 1..6: (1,0), (1,1),
+// (2,1), (2,2), (3,2), (3,3)).
 template <int D, bool Q8>
 int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     static const int forced = [] {
@@ -718,7 +728,8 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
         case 2: return launch_dma<D, 1, 1, Q8>(p, stream);
         case 3: return launch_dma<D, 2, 1, Q8>(p, stream);
         case 4: return launch_dma<D, 2, 2, Q8>(p, stream);
-        default: return launch_dma<D, 3, 3, Q8>(p, stream);  // 5 as well: (3,2) spills
+        case 5: return launch_dma<D, 3, 2, Q8>(p, stream);
+        default: return launch_dma<D, 3, 3, Q8>(p, stream);
     }
 }
 
