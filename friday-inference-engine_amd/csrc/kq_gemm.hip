@@ -77,12 +77,17 @@ struct WBlock {
     float ws[2], c[2];
 };
 
+// Word i / 4 of the 12 scale bytes (s0, s1, s2), chosen with bit masks: a select on a
+// wave-uniform index becomes a branch, which would split the stage's MFMAs from its decode.
+__device__ __forceinline__ uint32_t pick3(int i, uint32_t s0, uint32_t s1, uint32_t s2) {
+    const uint32_t m0 = 0u - (uint32_t)(i < 4), m2 = 0u - (uint32_t)(i >= 8);
+    return (s0 & m0) | (s1 & ~(m0 | m2)) | (s2 & m2);
+}
+
 // get_scale_min_k4: 6-bit scale and min of block j (0..7) of a Q4_K / Q5_K superblock
 __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc, int& m) {
-    auto byte = [&](int i) {
-        const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-        return (int)((w >> (8 * (i & 3))) & 0xFF);
-    };
+    auto byte = [&](int i) { return (int)((pick3(i, s0, s1, s2) >> (8 * (i & 3))) & 0xFF); };
+    // (a scalar branch on the stage-uniform j: measured faster than blending both forms)
     if (j < 4) {
         sc = byte(j) & 63;
         m = byte(j + 4) & 63;
@@ -175,9 +180,8 @@ __device__ __forceinline__ void decode_wraw(const WRaw& r, int blk, WBlock& o) {
             const uint32_t hb = (r.b[w] >> (4 * h + s)) & 0x01010101u;
             o.u[w] = lo | (hb << 2);  // q + 4, 0..7
         }
-        auto byte = [&](int i) {  // selects, not an indexed array (which would live in scratch)
-            const uint32_t w = i < 4 ? r.s[0] : (i < 8 ? r.s[1] : r.s[2]);
-            return (int)((w >> (8 * (i & 3))) & 0xFF);
+        auto byte = [&](int i) {  // masks, not an indexed array (which would live in scratch)
+            return (int)((pick3(i, r.s[0], r.s[1], r.s[2]) >> (8 * (i & 3))) & 0xFF);
         };
         const float d = half_bits(r.d);
 #pragma unroll
@@ -372,8 +376,10 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
         const int t = min(t0 + r, p.T - 1);
         xoff[i] = (uint32_t)(((size_t)t * p.K + (((lane & 7) ^ ((r >> 1) & 7)) * 8)) * 2);
     }
-    const bool w_wave = __builtin_amdgcn_readfirstlane(w_role);
-    const bool x_wave = __builtin_amdgcn_readfirstlane(x_role);
+    // every wave has a role when the tile shape gives one to every thread: then the role
+    // tests are compile-time true (no branch splits the stage's MFMAs from its decode)
+    const bool w_wave = 2 * BN >= NT ? true : (bool)__builtin_amdgcn_readfirstlane(w_role);
+    const bool x_wave = NT - 2 * BT <= 0 ? true : (bool)__builtin_amdgcn_readfirstlane(x_role);
 
     // raw operands of one stage in registers; two sets, so that the loads of stage s + 2
     // are in flight across the MFMAs of stage s and the decode of stage s + 1
@@ -461,7 +467,24 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
     store_stage(raw0, sbeg, sw0, sx0);
     wait_x();
     __syncthreads();
-    for (int st = 0; st < nst; st += 2) {
+    int st = 0;
+    // steady state (every guard below true, no branch between a stage's MFMAs and the decode
+    // of the next): measured 4-8 % faster than the guarded loop alone on Q4_K / Q2_K / Q3_K
+    for (; st + 3 < nst; st += 2) {
+        if (XH) load_xh(sbeg + st + 1, sx1);
+        load_stage(raw0, sbeg + st + 2);
+        compute(sw0, sx0);
+        store_stage(raw1, sbeg + st + 1, sw1, sx1);
+        wait_x();
+        __syncthreads();
+        if (XH) load_xh(sbeg + st + 2, sx0);
+        load_stage(raw1, sbeg + st + 3);
+        compute(sw1, sx1);
+        store_stage(raw0, sbeg + st + 2, sw0, sx0);
+        wait_x();
+        __syncthreads();
+    }
+    for (; st < nst; st += 2) {
         if (XH && st + 1 < nst) load_xh(sbeg + st + 1, sx1);
         if (st + 2 < nst) load_stage(raw0, sbeg + st + 2);
         compute(sw0, sx0);
