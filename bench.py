@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the KV-cache path on one MI355X (BASELINE.json metric and configs).
 
-Default (the driver's line): BASELINE config 3, the headline. A step is one
+Default (the driver's line): benchmark config 3, the headline. A step is one
 decode token through all 64 layers at Qwen2.5-32B attention shapes (40 query /
 8 kv heads, head_dim 128, fp16 KV, context 32768 after the append, all 64
 layers' caches resident in HBM, 8 GiB): per layer ONE launch of
@@ -19,7 +19,7 @@ stream the graph runs on. `cpu_baseline` times the reference's own CPU
 attention (cpu_ops.cpp decodeAttention compiled from source into oracle/_ref)
 on this host.
 
---config all additionally prints one JSON line per other BASELINE config
+--config all additionally prints one JSON line per other benchmark config
 (1: Qwen2.5-0.5B shapes; 2: 32 layers at 1k/4k/8k, cold and warm; 3 at 16k;
 4: chunked prefill on MFMA with MFMA utilisation; 5: 16 paged sequences).
 """
@@ -229,7 +229,7 @@ def headline(cx, args):
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic: device-generated N(0,1) fp16 K/V caches, seeded N(0,1) q/k/v",
-        "config": {"workload": f"BASELINE config 3 (headline): decode step over {L} layers, one launch per layer "
+        "config": {"workload": f"benchmark config 3 (headline): decode step over {L} layers, one launch per layer "
                                f"(RoPE + KV append + split-K GQA attention + LSE merge), ctx {S} after the append, "
                                f"{Hq}q/{Hkv}kv d{d}, fp16 KV, batch 1, HIP graph replay",
                    "layers": L, "ctx": S, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": d},
@@ -262,7 +262,7 @@ def decode_config(cx, name, S, L, Hq, Hkv, d, steps, warmup, cold):
 
 
 def prefill_config(cx, p0, steps, warmup, q8=False):
-    """512-token causal chunk after p0 cached tokens, 40q/8kv d128, MFMA.
+    """benchmark config 4: 512-token causal chunk after p0 cached tokens, 40q/8kv d128, MFMA.
     q8: int8 caches with one fp16 scale per 32 values (random codes, scales of 0.01 scale)."""
     import numpy as np
 
@@ -464,7 +464,7 @@ def q8_config(cx, S, L, steps, warmup):
 
 
 def paged_config(cx, steps, warmup):
-    """16 sequences, S ~ U[256, 16k], 16-token pages in a permuted pool, one launch."""
+    """benchmark config 5: 16 sequences, S ~ U[256, 16k], 16-token pages in a permuted pool, one launch."""
     import numpy as np
 
     fa = cx.fa
@@ -516,7 +516,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm", "layer"), default="headline",
-                    help="headline: the driver's one line; all/others: also (only) the other BASELINE configs")
+                    help="headline: the driver's one line; all/others: also (only) the other benchmark configs of BASELINE.json")
     args = ap.parse_args()
 
     if args.gpus != 1:

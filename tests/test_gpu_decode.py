@@ -3,7 +3,7 @@
 Mirrors tests/kernels/test_decode_attention.cu of the reference (Qwen2.5-32B
 shapes 40q/8kv d128, q = 2*N(0,1), seq in {1, 2, 17, 255, 256, 257, 300, 1000,
 2048}, single-pass and split-K with host and device lengths) and adds the
-BASELINE configs and the closed-form cases of the softmax rules.
+the benchmark configs of BASELINE.json and the closed-form cases of the softmax rules.
 """
 import numpy as np
 import pytest
@@ -91,7 +91,7 @@ def test_shapes(gpu, oracle, Hq, Hkv, d, S):
 
 @pytest.mark.parametrize("S", [1024, 4096, 8192])
 def test_config2_outliers(gpu, oracle, S):
-    """32q/8kv d128, ~1% of cached K rows x30 (FP32-safe softmax)."""
+    """benchmark config 2: 32q/8kv d128, ~1% of cached K rows x30 (FP32-safe softmax)."""
     fa = gpu
     Hq, Hkv, d = 32, 8, 128
     rng = np.random.default_rng(1000 + S)
@@ -110,7 +110,7 @@ def test_config2_outliers(gpu, oracle, S):
 
 @pytest.mark.parametrize("S", [16384, 32768])
 def test_config3_long_context(gpu, oracle, S):
-    """BASELINE config 3 (headline): 40q/8kv d128 at 16k / 32k, split-K + LSE merge."""
+    """benchmark config 3 (headline): 40q/8kv d128 at 16k / 32k, split-K + LSE merge."""
     fa = gpu
     Hq, Hkv, d = 40, 8, 128
     rng = np.random.default_rng(S)

@@ -1,4 +1,4 @@
-"""GPU parity of paged multi-sequence append + decode.
+"""GPU parity of paged multi-sequence append + decode (benchmark config 5).
 
 16-token pages with physical ids from a seeded permutation, one block table row
 per sequence. Bar: every sequence bit-identical to the contiguous-cache split

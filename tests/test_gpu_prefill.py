@@ -2,7 +2,7 @@
 
 Mirrors tests/kernels/test_prefill_attention.cu: the same (nh, nkv, T, p0, int8)
 cases with max_ctx 1024; row t must equal decode attention at S = p0 + t + 1
-(the oracle computes exactly that, in the reference CPU order). Adds BASELINE
+(the oracle computes exactly that, in the reference CPU order). Adds benchmark
 config 4 (40q/8kv, T = 512, p0 up to 7680) on sampled rows and the causal
 invariance: K/V rows after a query's position do not change its output.
 """
@@ -101,7 +101,7 @@ def test_q8_scales_off_dword_alignment(gpu, oracle):
 
 @pytest.mark.parametrize("p0", [0, 1024, 7680])
 def test_config4_chunk(gpu, oracle, p0):
-    """40q/8kv d128, 512-token chunk after p0 cached tokens; sampled rows vs decode oracle."""
+    """benchmark config 4: 40q/8kv d128, 512-token chunk after p0 cached tokens; sampled rows vs decode oracle."""
     fa = gpu
     Hq, Hkv, d, T = 40, 8, 128, 512
     rng = np.random.default_rng(p0 + 4)

@@ -95,7 +95,7 @@ def test_step_workspace_rearms(gpu, oracle):
 
 
 def test_paged_step_matches_contiguous_step(gpu):
-    """BASELINE config 5 in one launch: every sequence equals the contiguous step bit for bit."""
+    """benchmark config 5 in one launch: every sequence equals the contiguous step bit for bit."""
     from test_gpu_paged import build_paged
     fa = gpu
     Hq, Hkv, d, nseq, PAGE = 40, 8, 128, 9, 16
