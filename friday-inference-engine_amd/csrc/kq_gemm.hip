@@ -626,9 +626,9 @@ __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, gv_lds_u
 // blocks l, l + 64, ...; returns the wave-summed fp32 dot product (every lane).
 template <int KIND>
 __device__ __forceinline__ float gemv_row(const unsigned char* wrow, const int8_t* xq, const float* xd, int nblk,
-                                          int lane) {
+                                          int lane, int first = 0, int step = 64) {
     float acc = 0.0f;
-    for (int blk = lane; blk < nblk; blk += 64) {
+    for (int blk = first + lane; blk < nblk; blk += step) {
         WRaw r;
         load_wraw<KIND>(wrow, blk, r);
         const uint4 xa = *reinterpret_cast<const uint4*>(xq + 32 * blk);
@@ -668,8 +668,8 @@ __device__ __forceinline__ void copy_span(const void* src, uint32_t span, gv_lds
         dma4(static_cast<const uint8_t*>(src), min(rest0 + 256 * i + 4 * lane, span - 4), lds + rest0 + 256 * i);
 }
 
-template <int KIND, int ROWS, bool XL>
-__global__ __launch_bounds__(64 * ROWS) void kq_gemv_lds_kernel(KqGemvParams p) {
+template <int KIND, int ROWS, bool XL, int WPR>
+__global__ __launch_bounds__(64 * ROWS * WPR) void kq_gemv_lds_kernel(KqGemvParams p) {
     extern __shared__ __align__(16) unsigned char rows_lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -688,22 +688,36 @@ __global__ __launch_bounds__(64 * ROWS) void kq_gemv_lds_kernel(KqGemvParams p) 
     const uint32_t span = (uint32_t)(nrows * p.row_bytes);
     const uint8_t* src = W + (size_t)n0 * p.row_bytes;  // 4-byte aligned: W is, n0 is even, row_bytes even
     gv_lds_u8* lds = (gv_lds_u8*)rows_lds;
-    copy_span(src, span, lds, wave, ROWS, lane);
+    constexpr int NW = ROWS * WPR;  // waves; wave w takes row w % ROWS, block slice w / ROWS
+    copy_span(src, span, lds, wave, NW, lane);
     // XL: the activations (xq: K bytes, 16-byte aligned; xd: K / 8 bytes) after the rows, at
     // xoff = ROWS row_bytes rounded up to 256
     const uint32_t xoff = ((ROWS * (uint32_t)p.row_bytes + 255) / 256) * 256;
     if constexpr (XL) {
-        copy_span(p.xq, (uint32_t)p.K, lds + xoff, wave, ROWS, lane);
-        copy_span(p.xd, (uint32_t)p.K / 8, lds + xoff + p.K, wave, ROWS, lane);
+        copy_span(p.xq, (uint32_t)p.K, lds + xoff, wave, NW, lane);
+        copy_span(p.xd, (uint32_t)p.K / 8, lds + xoff + p.K, wave, NW, lane);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (wave >= nrows) return;
-    const int row = n0 + wave;
-    const unsigned char* wrow = rows_lds + (size_t)wave * p.row_bytes;
+    const int rw = wave % ROWS, slice = wave / ROWS;
     const int8_t* xq = XL ? reinterpret_cast<const int8_t*>(rows_lds + xoff) : p.xq;
     const float* xd = XL ? reinterpret_cast<const float*>(rows_lds + xoff + p.K) : p.xd;
-    const float acc = gemv_row<KIND>(wrow, xq, xd, p.K / 32, lane);
+    float acc = 0.0f;
+    if (rw < nrows)
+        acc = gemv_row<KIND>(rows_lds + (size_t)rw * p.row_bytes, xq, xd, p.K / 32, lane, 64 * slice, 64 * WPR);
+    if constexpr (WPR > 1) {
+        // the slices of a row add in slice order (the same for every call); the partial sums
+        // sit past the activations
+        __shared__ float part[ROWS * WPR];
+        if (lane == 0) part[wave] = acc;
+        __syncthreads();
+        if (slice != 0) return;
+        acc = part[rw];
+#pragma unroll
+        for (int k = 1; k < WPR; ++k) acc += part[rw + k * ROWS];
+    }
+    if (rw >= nrows) return;
+    const int row = n0 + rw;
     if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
 }
 
@@ -840,16 +854,16 @@ int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
     return launch_kq_shape<2, 2, 1, 1>(kind, p, stream);
 }
 
-template <int ROWS, bool XL>
+template <int ROWS, bool XL, int WPR = 1>
 int launch_gemv_lds(int kind, const KqGemvParams& p, size_t lds, hipStream_t stream) {
-    const dim3 grid(((p.N + ROWS - 1) / ROWS) * (p.W2 ? 2 : 1)), block(64 * ROWS);
+    const dim3 grid(((p.N + ROWS - 1) / ROWS) * (p.W2 ? 2 : 1)), block(64 * ROWS * WPR);
     switch (kind) {
-        case kKqQ2K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ2K, ROWS, XL>), grid, block, lds, stream, p); break;
-        case kKqQ3K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ3K, ROWS, XL>), grid, block, lds, stream, p); break;
-        case kKqQ4K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ4K, ROWS, XL>), grid, block, lds, stream, p); break;
-        case kKqQ5K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ5K, ROWS, XL>), grid, block, lds, stream, p); break;
-        case kKqQ6K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ6K, ROWS, XL>), grid, block, lds, stream, p); break;
-        case kKqQ80: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ80, ROWS, XL>), grid, block, lds, stream, p); break;
+        case kKqQ2K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ2K, ROWS, XL, WPR>), grid, block, lds, stream, p); break;
+        case kKqQ3K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ3K, ROWS, XL, WPR>), grid, block, lds, stream, p); break;
+        case kKqQ4K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ4K, ROWS, XL, WPR>), grid, block, lds, stream, p); break;
+        case kKqQ5K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ5K, ROWS, XL, WPR>), grid, block, lds, stream, p); break;
+        case kKqQ6K: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ6K, ROWS, XL, WPR>), grid, block, lds, stream, p); break;
+        case kKqQ80: hipLaunchKernelGGL((kq_gemv_lds_kernel<kKqQ80, ROWS, XL, WPR>), grid, block, lds, stream, p); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -857,8 +871,9 @@ int launch_gemv_lds(int kind, const KqGemvParams& p, size_t lds, hipStream_t str
 
 // The LDS-staged GEMV when its rows (and activations) fit in 64 KiB (two or more workgroups
 // per CU) and every row group spans a multiple of 4 bytes, else one wave per row straight
-// from memory. FRIDAY_GEMV_LDS = 0 forces the direct kernel; FRIDAY_GEMV_ROWS (2 / 4 / 8)
-// and FRIDAY_GEMV_XL (0 / 1) override the rows per workgroup and the activation staging.
+// from memory. FRIDAY_GEMV_LDS = 0 forces the direct kernel; FRIDAY_GEMV_ROWS (2 / 4 / 8),
+// FRIDAY_GEMV_XL (0 / 1) and FRIDAY_GEMV_WPR (1 / 2, with 4 rows) override the rows per
+// workgroup, the activation staging and the waves per row.
 int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream) {
     static const int env_lds = [] {
         const char* e = std::getenv("FRIDAY_GEMV_LDS");
@@ -871,6 +886,10 @@ int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream) {
     static const int env_xl = [] {
         const char* e = std::getenv("FRIDAY_GEMV_XL");
         return e && *e ? std::atoi(e) : -1;
+    }();
+    static const int env_wpr = [] {
+        const char* e = std::getenv("FRIDAY_GEMV_WPR");
+        return e && *e ? std::atoi(e) : 0;
     }();
     const int rows = p.W2 ? 2 * p.N : p.N;
     int nr = env_rows == 2 || env_rows == 4 || env_rows == 8 ? env_rows : 4;
@@ -888,6 +907,11 @@ int launch_kq_gemv(int kind, const KqGemvParams& p, hipStream_t stream) {
     if (env_lds != 0 && span4 && lds <= 65536) {
         if (nr == 2) return xl ? launch_gemv_lds<2, true>(kind, p, lds, stream) : launch_gemv_lds<2, false>(kind, p, lds, stream);
         if (nr == 8) return xl ? launch_gemv_lds<8, true>(kind, p, lds, stream) : launch_gemv_lds<8, false>(kind, p, lds, stream);
+        // two waves per row (alternate 64-block slices) for long rows: measured 6 % faster at
+        // K = 14336 (448 blocks), 6 % slower at K = 5120 (160 blocks, half the lanes idle)
+        const int wpr = env_wpr > 0 ? env_wpr : (p.K / 32 >= 384 ? 2 : 1);
+        if (wpr == 2)
+            return xl ? launch_gemv_lds<4, true, 2>(kind, p, lds, stream) : launch_gemv_lds<4, false, 2>(kind, p, lds, stream);
         return xl ? launch_gemv_lds<4, true>(kind, p, lds, stream) : launch_gemv_lds<4, false>(kind, p, lds, stream);
     }
     const dim3 grid((rows + 3) / 4), block(256);
