@@ -163,7 +163,7 @@ def test_gemv_two_matrices_bias(gpu, oracle):
 # ---- K split (shapes whose 128 x 128 tiles do not fill the GPU): fp32 partials in the
 # library's per-stream workspace, summed in split order by the last workgroup of a tile.
 
-SPLIT_SHAPES = [(256, 4096, 512, 3), (200, 2048, 384, 5), (512, 3072, 256, 6)]
+SPLIT_SHAPES = [(256, 4096, 512, 3), (200, 2048, 384, 5), (512, 3072, 256, 6), (160, 4096, 300, 1)]
 
 
 @pytest.mark.parametrize("T,K,N,kind", SPLIT_SHAPES)
