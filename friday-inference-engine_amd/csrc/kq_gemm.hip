@@ -389,11 +389,11 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
         float xs;
     };
     Raw raw0, raw1;
-    // XH copy of stage st into the tile sx. Issued before the weight loads of stage st + 1
-    // (in program order), so it is older than them: the compiler's wait for those registers,
-    // before they are decoded into LDS ahead of the barrier that publishes stage st, leaves
-    // only younger loads outstanding (loads complete in order), i.e. this copy has landed.
-    // Waves without a weight role wait explicitly (wait_x below).
+    // XH copy of stage st into the tile sx, issued one stage ahead. Every wave waits for all
+    // of its vector memory operations (s_waitcnt vmcnt(0)) before the barrier that publishes
+    // the stage: a partial count does not cover a global->LDS copy (measured: a ring of such
+    // copies waited with constant partial counts read stale tiles now and then), and the full
+    // wait costs nothing measurable here.
     auto load_xh = [&](int st, unsigned char* sx) __attribute__((always_inline)) {
         if (x_wave) {
             const uint16_t* base = p.xh + (size_t)st * kGBK;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
         }
     };
     auto wait_x = [&]() __attribute__((always_inline)) {
-        if (XH && !w_wave) wait_vmem();
+        if (XH) wait_vmem();
     };
     auto load_stage = [&](Raw& r, int st) __attribute__((always_inline)) {
         const int blk = st * (kGBK / 32) + lh;
@@ -459,8 +459,8 @@ __global__ __launch_bounds__(64 * WVN * WVT) void kq_gemm_kernel(KqGemmParams p)
     // stage st: loads of st + 2 into the set that held st, MFMAs on LDS buffer st % 2,
     // decode of st + 1 (loaded one stage earlier) into the other buffer, barrier
     // (st counts from the split's first stage)
-    // (XH: the activation copy of stage st + 1 is issued at the top of stage st, before the
-    // weight loads of stage st + 2, into the buffer that stage st - 1 used)
+    // (XH: the activation copy of stage st + 1 is issued at the top of stage st, into the
+    // buffer that stage st - 1 used, and waited for before the barrier that ends stage st)
     if (XH) load_xh(sbeg, sx0);
     load_stage(raw0, sbeg);
     if (nst > 1) load_stage(raw1, sbeg + 1);
