@@ -128,6 +128,33 @@ def test_config3_long_context(gpu, oracle, S):
         assert np.array_equal(c.result(), split), f"fused call {rep}"
 
 
+@pytest.mark.parametrize("S", [131072, 100003])
+def test_max_context_many_splits(gpu, oracle, S):
+    """A 128k-position cache (Qwen2.5's longest context) with 2 kv heads of group 5: 128 splits
+    of 1024 positions at S = 131072 and 112 of 896 at S = 100003, so the merge takes its
+    general path (more than 32 splits). Host-length, device-position and fused-merge calls
+    give the same bits, and match the oracle."""
+    fa = gpu
+    Hq, Hkv, d, max_ctx = 10, 2, 128, 131072
+    rng = np.random.default_rng(S)
+    kc = f16(rng, (S, Hkv * d))
+    vc = f16(rng, (S, Hkv * d))
+    q = f16(rng, Hq * d)
+    c = Cache(fa, q, kc, vc, Hq, max_ctx)
+    ref = oracle.decode(q, kc, vc, S, Hq, Hkv, d)
+    fa.launchDecodeAttentionSplit(c.q, c.k, c.v, c.out, S, None, max_ctx, Hq, Hkv, d, c.ws)
+    host = c.result()
+    assert_close(host, ref, f"max context S={S}")
+    c.pos.upload(np.array([S - 1], np.int32))
+    c.out.fill_bytes(0xFF)
+    fa.launchDecodeAttentionSplit(c.q, c.k, c.v, c.out, 0, c.pos, max_ctx, Hq, Hkv, d, c.ws)
+    assert np.array_equal(c.result(), host), "device-position call differs from host-length call"
+    for rep in range(2):
+        c.out.fill_bytes(0xFF)
+        fa.launchDecodeAttentionFused(c.q, c.k, c.v, c.out, 0, c.pos, max_ctx, Hq, Hkv, d, c.wsf)
+        assert np.array_equal(c.result(), host), f"fused call {rep} differs from the merge kernel"
+
+
 def test_closed_forms(gpu, oracle):
     """Exact cases fixed by the softmax rules (cpu_ops.cpp:45-83)."""
     fa = gpu
