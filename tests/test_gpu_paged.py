@@ -49,7 +49,8 @@ def contiguous_decode(fa, q, kc, vc, S, Hq, Hkv, d, max_seq):
 
 
 @pytest.mark.parametrize("nseq,lo,hi,Hq,Hkv,d", [(6, 1, 3000, 40, 8, 128), (16, 256, 4096, 40, 8, 128),
-                                                 (5, 17, 700, 14, 2, 64)])
+                                                 (5, 17, 700, 14, 2, 64),
+                                                 (4, 6000, 40000, 10, 2, 128)])  # 47..128 splits: general merge
 def test_paged_matches_contiguous(gpu, oracle, nseq, lo, hi, Hq, Hkv, d):
     fa = gpu
     rng = np.random.default_rng(nseq * 1000 + hi)
