@@ -218,11 +218,14 @@ def test_gqa_heads_share_kv(gpu):
     assert np.array_equal(got, np.repeat(got[:, :1], Hq // Hkv, axis=1))
 
 
-def test_int8_decode(gpu, oracle):
-    """int8 KV with fp16 scales per 32 values (k_scale/v_scale path)."""
+@pytest.mark.parametrize("Hq,Hkv,d,S", [(40, 8, 128, 1000),
+                                         (14, 2, 64, 513),
+                                         (10, 2, 128, 60000)])  # 118 splits: general merge
+def test_int8_decode(gpu, oracle, Hq, Hkv, d, S):
+    """int8 KV with fp16 scales per 32 values (k_scale/v_scale path); the fused merge gives
+    the merge kernel's bits."""
     fa = gpu
-    Hq, Hkv, d, S = 40, 8, 128, 1000
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(5 + S)
     k8 = rng.integers(-127, 128, (S, Hkv * d), dtype=np.int8)
     v8 = rng.integers(-127, 128, (S, Hkv * d), dtype=np.int8)
     ks = rng.uniform(0.005, 0.03, (S, Hkv * d // 32)).astype(np.float16).view(np.uint16)
@@ -236,4 +239,11 @@ def test_int8_decode(gpu, oracle):
     ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, S))
     fa.launchDecodeAttentionSplit(dq, dk, dv, out, S, None, S, Hq, Hkv, d, ws, k_scale=dks, v_scale=dvs)
     fa.Hip.sync()
-    assert_close(as_f32(out.download(Hq * d, np.uint16)), ref, "int8 decode")
+    split = out.download(Hq * d, np.uint16)
+    assert_close(as_f32(split), ref, "int8 decode")
+    wsf = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, S))
+    fa.decodeWorkspaceInit(wsf)
+    out.fill_bytes(0xFF)
+    fa.launchDecodeAttentionFused(dq, dk, dv, out, S, None, S, Hq, Hkv, d, wsf, k_scale=dks, v_scale=dvs)
+    fa.Hip.sync()
+    assert np.array_equal(out.download(Hq * d, np.uint16), split), "int8 fused merge differs from the merge kernel"
