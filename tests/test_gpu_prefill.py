@@ -113,6 +113,22 @@ def test_config4_chunk(gpu, oracle, p0):
         assert_close(got[t], ref, f"config4 p0={p0} t={t}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,d,T,p0,q8", [(10, 2, 128, 77, 100000, False), (10, 2, 128, 77, 60000, True),
+                                               (14, 2, 64, 200, 30000, False)])
+def test_long_prefix(gpu, oracle, Hq, Hkv, d, T, p0, q8):
+    """A ragged chunk after a long cached prefix (up to 100k positions): sampled rows vs the
+    decode oracle at S = p0 + t + 1."""
+    fa = gpu
+    rng = np.random.default_rng(p0 + T)
+    q = f16(rng, (T, Hq * d))
+    k, v, ks, vs = make_cache(rng, p0 + T, Hkv * d, q8)
+    got = run_prefill(fa, q, k, v, ks, vs, T, p0, Hq, Hkv, d)
+    for t in sorted(set([0, 1, 15, 16, T - 1] + list(rng.choice(T, 3, replace=False)))):
+        S = p0 + t + 1
+        ref = oracle.decode_q8(q[t], k, ks, v, vs, S, Hq, Hkv, d) if q8 else oracle.decode(q[t], k, v, S, Hq, Hkv, d)
+        assert_close(got[t], ref, f"long prefix p0={p0} t={t} q8={q8}")
+
+
 def test_causal_invariance(gpu):
     """Rows after a query's position must not influence it (bit-identical output)."""
     fa = gpu
