@@ -376,6 +376,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     h8 nk[NH], nkp[NH], nv[NH];
     float2 ncs[ROPE ? CW : 1];
     int append_wave = -1, append_tile = -1, append_row = -1;
+    // q is rotated only when position S-1 is the new token's own position inside the cache,
+    // as the separate append does (it skips positions < 0 and >= max_ctx)
+    bool rot_q = false;
     const int nchunk = (lane % Gm::CPR) * CW;  // first element of this lane's row chunk
     if constexpr (ROPE) {
         const int pos = S > 0 ? S - 1 : 0;
@@ -389,7 +392,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         // the wave that loads the tile holding position S-1 (in the split holding it)
         // takes the new row from registers instead of the cache; past max_seq: no append
         const int s_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
-        if (S > 0 && split == nsp - 1 && s_raw == S) {
+        rot_q = S > 0 && s_raw == S;
+        if (rot_q && split == nsp - 1) {
             const int last_tile = (end - start - 1) / kTile;
             append_wave = last_tile % kWaves;
             append_tile = last_tile;
@@ -421,7 +425,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     float ksc = 0.0f, vsc = 0.0f;
     auto prepare = [&]() __attribute__((always_inline)) {
         if constexpr (ROPE) {
-            if (p.neox) {
+            if (!rot_q) {
+                // position outside the cache: q keeps its values, no row is appended
+            } else if (p.neox) {
 #pragma unroll
                 for (int s = 0; s < Gm::KSTEPS / 2; ++s)
 #pragma unroll

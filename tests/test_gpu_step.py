@@ -69,6 +69,41 @@ def test_step_matches_two_launches(gpu, oracle, Hq, Hkv, d, S, max_ctx, base, ne
     run_step_vs_two_launch(gpu, oracle, Hq, Hkv, d, S, max_ctx, base, neox, devpos, seed=S + Hq)
 
 
+@pytest.mark.parametrize("over,neox", [(0, 1), (3, 0)])
+def test_step_position_past_cache(gpu, over, neox):
+    """*d_pos >= max_ctx: the separate append skips the token (q stays unrotated, no row is
+    written), then attention covers the max_ctx cached rows. The step does the same, bit for
+    bit."""
+    fa = gpu
+    Hq, Hkv, d, max_ctx = 40, 8, 128, 4096
+    rng = np.random.default_rng(77 + over)
+    kv_dim = Hkv * d
+    kc, vc = f16(rng, (max_ctx, kv_dim)), f16(rng, (max_ctx, kv_dim))
+    q, k, v = f16(rng, (1, Hq * d)), f16(rng, (1, kv_dim)), f16(rng, (1, kv_dim))
+    dt = fa.DeviceBuffer.from_array(fa.rope_table_host(max_ctx, d, 1e6))
+    dpos = fa.DeviceBuffer.from_array(np.array([max_ctx + over], np.int32))
+    ws_bytes = fa.splitAttentionWorkspaceBytes(Hq, max_ctx)
+    outs, bufs = [], []
+    for fused in (True, False):
+        b = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q, k=k, v=v, kc=kc, vc=vc).items()}
+        out, ws = fa.DeviceBuffer(q.nbytes), fa.DeviceBuffer(ws_bytes)
+        fa.decodeWorkspaceInit(ws)
+        if fused:
+            fa.decodeStep(b["q"], b["k"], b["v"], b["kc"], b["vc"], out, dpos, 0, max_ctx, Hq, Hkv, d, dt, neox, ws)
+        else:
+            fa.ropeStoreKv(b["q"], b["k"], b["v"], b["kc"], b["vc"], dpos, 0, 1, d, Hq, Hkv, max_ctx, dt, neox)
+            fa.launchDecodeAttentionFused(b["q"], b["kc"], b["vc"], out, 0, dpos, max_ctx, Hq, Hkv, d, ws)
+        outs.append(out)
+        bufs.append(b)
+    fa.Hip.sync()
+    for name, b in zip(("step", "two launches"), bufs):
+        assert np.array_equal(b["q"].download(q.shape, np.uint16), q), f"{name}: q changed"
+        assert np.array_equal(b["kc"].download(kc.shape, np.uint16), kc), f"{name}: k cache changed"
+        assert np.array_equal(b["vc"].download(vc.shape, np.uint16), vc), f"{name}: v cache changed"
+    g1, g2 = (o.download(Hq * d, np.uint16) for o in outs)
+    assert np.array_equal(g1, g2), "step differs from the two-launch sequence"
+
+
 def test_step_workspace_rearms(gpu, oracle):
     """Counters return to zero: consecutive steps on one workspace keep the bits."""
     fa = gpu
