@@ -124,3 +124,25 @@ def test_store_kv_q8(gpu, oracle, T, pos0, kv_dim):
     oracle.store_kv_q8(k, v, k8, ks, v8, vs, pos0, kv_dim)
     for g, e, name in zip(got, (k8, ks, v8, vs), ("k8", "k_scale", "v8", "v_scale")):
         assert np.array_equal(g, e), name
+
+
+def test_store_kv_q8_past_cache(gpu, oracle):
+    """A device position near the end of the cache: tokens at or beyond max_ctx are skipped,
+    the ones before are written, and rows after the cache (a guard region) stay untouched."""
+    fa = gpu
+    T, pos0, kv_dim, max_ctx, guard = 6, 60, 1024, 63, 5
+    rng = np.random.default_rng(63)
+    k, v = f16(rng, (T, kv_dim), 2.0), f16(rng, (T, kv_dim))
+    k8 = np.full((max_ctx + guard, kv_dim), 99, np.int8)
+    v8 = k8.copy()
+    ks = np.full((max_ctx + guard, kv_dim // 32), CANARY, np.uint16)
+    vs = ks.copy()
+    bufs = [fa.DeviceBuffer.from_array(a) for a in (k, v, k8, ks, v8, vs)]
+    dpos = fa.DeviceBuffer.from_array(np.array([pos0], np.int32))
+    fa.storeKvQ8(bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], bufs[5], dpos, 0, T, kv_dim, max_ctx)
+    fa.Hip.sync()
+    got = [bufs[i].download(a.shape, a.dtype) for i, a in ((2, k8), (3, ks), (4, v8), (5, vs))]
+    n = max_ctx - pos0  # tokens inside the cache
+    oracle.store_kv_q8(k[:n], v[:n], k8, ks, v8, vs, pos0, kv_dim)
+    for g, e, name in zip(got, (k8, ks, v8, vs), ("k8", "k_scale", "v8", "v_scale")):
+        assert np.array_equal(g, e), name
