@@ -111,3 +111,32 @@ def test_paged_append_then_decode(gpu, oracle):
         assert np.array_equal(got_kp[phys, pos % PAGE], kc[pos]), f"k row seq {b}"
         assert np.array_equal(got_vp[phys, pos % PAGE], vc[pos]), f"v row seq {b}"
         assert_close(got[b], oracle.decode(qb[0], kc, vc, S, Hq, Hkv, d), f"paged seq {b}")
+
+
+def test_paged_empty_sequence(gpu, oracle):
+    """A sequence of length 0 in the batch: no positions, so its output is zero (the combine
+    rule out = L > 1e-12 ? O / L : 0); the other sequences are unaffected."""
+    fa = gpu
+    Hq, Hkv, d = 40, 8, 128
+    rng = np.random.default_rng(404)
+    lens = [0, 5, 1000, 0]
+    max_seq = 1024
+    seqs, table, k_pool, v_pool = build_paged(rng, lens, Hkv * d, max_seq)
+    q = f16(rng, (len(lens), Hq * d))
+    dq = fa.DeviceBuffer.from_array(q)
+    dk, dv = fa.DeviceBuffer.from_array(k_pool), fa.DeviceBuffer.from_array(v_pool)
+    dt = fa.DeviceBuffer.from_array(table)
+    dl = fa.DeviceBuffer.from_array(np.array(lens, np.int32))
+    out = fa.DeviceBuffer(q.nbytes)
+    out.fill_bytes(0xFF)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(len(lens), Hq, max_seq))
+    fa.decodeWorkspaceInit(ws)
+    fa.launchPagedDecodeAttention(dq, dk, dv, out, dt, table.shape[1], dl, len(lens), max_seq, Hq, Hkv, d, ws)
+    fa.Hip.sync()
+    got = out.download((len(lens), Hq * d), np.uint16)
+    for b, S in enumerate(lens):
+        if S == 0:
+            assert (got[b] == 0).all(), f"empty sequence {b}: output not zero"
+        else:
+            kc, vc = seqs[b]
+            assert np.array_equal(got[b], contiguous_decode(fa, q[b], kc, vc, S, Hq, Hkv, d, max_seq)), f"seq {b}"
