@@ -114,10 +114,11 @@ def test_config4_chunk(gpu, oracle, p0):
 
 
 @pytest.mark.parametrize("Hq,Hkv,d,T,p0,q8", [(10, 2, 128, 77, 100000, False), (10, 2, 128, 77, 60000, True),
-                                               (14, 2, 64, 200, 30000, False)])
+                                               (14, 2, 64, 200, 30000, False),
+                                               (10, 2, 128, 2048, 100, False), (10, 2, 128, 2047, 9, True)])
 def test_long_prefix(gpu, oracle, Hq, Hkv, d, T, p0, q8):
-    """A ragged chunk after a long cached prefix (up to 100k positions): sampled rows vs the
-    decode oracle at S = p0 + t + 1."""
+    """A ragged chunk after a long cached prefix (up to 100k positions), and chunks of about
+    2k tokens: sampled rows vs the decode oracle at S = p0 + t + 1."""
     fa = gpu
     rng = np.random.default_rng(p0 + T)
     q = f16(rng, (T, Hq * d))
