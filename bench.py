@@ -60,7 +60,7 @@ class Ctx:
         fa.load()
         if fa.Hip.device_count() < 1:
             raise SystemExit("no HIP device")
-        self.bk = C.CDLL(os.path.join(ROOT, "friday-inference-engine_amd", "lib", "libfa_benchkit.so"))
+        self.bk = C.CDLL(os.path.join(ROOT, "bench_kit", "libfa_benchkit.so"))
         self.bk.fabk_fill_normal_f16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
         self.stream = fa.Stream()
 
@@ -515,6 +515,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only copy 1 GiB three times with the bench-kit streaming copy (one 16-byte load and "
+                         "store per element): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run give the "
+                         "counters' reading for a known 1 GiB read + 1 GiB write")
     ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm", "layer"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other benchmark configs of BASELINE.json")
     args = ap.parse_args()
@@ -525,6 +529,15 @@ def main():
         sys.exit(2)
 
     cx = Ctx()
+    if args.calibrate:
+        cx.bk.fabk_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        n = 1 << 30
+        a, b = cx.fa.DeviceBuffer(n), cx.fa.DeviceBuffer(n)
+        for _ in range(3):
+            cx.bk.fabk_copy(a.ptr, b.ptr, n, cx.stream.s)
+        cx.stream.synchronize()
+        log(f"[bench] calibration: copied {n} bytes x3")
+        return
     if args.config in ("headline", "all"):
         print(json.dumps(headline(cx, args)), flush=True)
     if args.config in ("all", "others"):

@@ -1,4 +1,4 @@
-// Benchmark helpers (not part of the product ABI): device-side synthetic data
+// Benchmark helpers of bench.py (not part of the product ABI): device-side synthetic data
 // and a plain streaming copy used to calibrate the HBM byte counters.
 #include <hip/hip_runtime.h>
 #include <stdint.h>

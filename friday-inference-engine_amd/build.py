@@ -19,9 +19,10 @@ OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libfriday_attn.so")
 SOURCES = ["fa_api.cpp", "fa_append.hip", "fa_decode.hip", "fa_prefill.hip", "kq_gemm.hip"]
-# benchmark-only helpers (synthetic fill, calibration copy), a separate library
-BENCHKIT_SOURCES = ["fa_benchkit.hip"]
-BENCHKIT = os.path.join(LIB_DIR, "libfa_benchkit.so")
+# benchmark-only helpers (synthetic fill, counter-calibration copy): a separate library
+# next to bench.py, not part of the product
+BENCHKIT_SRC = os.path.join(HERE, "..", "bench_kit", "fa_benchkit.hip")
+BENCHKIT = os.path.join(HERE, "..", "bench_kit", "libfa_benchkit.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -51,10 +52,10 @@ SOURCE_FLAGS = {"fa_prefill.hip": _VGPR_MFMA, "fa_decode.hip": _VGPR_MFMA, "kq_g
 def _compile(sources, ex):
     objs, jobs = [], []
     for src in sources:
-        obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+        path = src if os.path.isabs(src) else os.path.join(CSRC, src)
+        obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
         objs.append(obj)
-        jobs.append(ex.submit(_run, [HIPCC, *CFLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src),
-                                     "-o", obj]))
+        jobs.append(ex.submit(_run, [HIPCC, *CFLAGS, *SOURCE_FLAGS.get(src, []), "-c", path, "-o", obj]))
     return objs, jobs
 
 
@@ -69,7 +70,7 @@ def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=8) as ex:
         objs, jobs = _compile(SOURCES, ex)
-        bobjs, bjobs = _compile(BENCHKIT_SOURCES, ex)
+        bobjs, bjobs = _compile([os.path.abspath(BENCHKIT_SRC)], ex)
         for j in jobs + bjobs:
             out = j.result()
             if verbose and out.strip():

@@ -367,7 +367,7 @@ static int paged_decode_common(const char* w, uint16_t* q, const uint16_t* k_new
     if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
     if (batch <= 0 || max_seq_len <= 0 || !q || !k_pool || !v_pool || !out || !block_table || !seq_lens)
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
-    if ((long long)block_table_stride * FA_PAGE_TOKENS < max_seq_len)
+    if (block_table_stride <= 0 || (long long)block_table_stride * FA_PAGE_TOKENS < max_seq_len)
         return fail(FA_ERR_INVALID, "%s: block_table_stride %d cannot address max_seq_len %d", w,
                     block_table_stride, max_seq_len);
     const int G = num_heads / num_kv_heads;
@@ -401,7 +401,7 @@ int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v,
     const char* w = "paged_rope_store_kv";
     if (int rc = check_heads(w, num_q_heads, num_kv_heads, head_dim)) return rc;
     if (batch <= 0 || max_ctx <= 0 || !q || !k || !v || !k_pool || !v_pool || !block_table || !seq_lens ||
-        !rope_table || block_table_stride * FA_PAGE_TOKENS < max_ctx)
+        !rope_table || block_table_stride <= 0 || (long long)block_table_stride * FA_PAGE_TOKENS < max_ctx)
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
     fa::RopeParams p{};
     p.q = q; p.k = k; p.v = v; p.k_dst = k_pool; p.v_dst = v_pool; p.table = rope_table;
@@ -513,27 +513,14 @@ int friday_gemm_q8_reserve(int T, int K, int N, void* stream) {
     return ok();
 }
 
-int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
-                   int ldy, void* stream, const float* bias, const uint16_t* res) {
-    const char* w = "gemm_q8";
-    if (!friday_gemm_q8_supported(kind, K))
-        return fail(FA_ERR_UNSUPPORTED, "%s: unsupported type %d or K=%d (K must be a multiple of 256)", w, kind, K);
-    if (T <= 0) return ok();
-    if (N <= 0 || ldy < N) return fail(FA_ERR_INVALID, "%s: invalid N=%d / ldy=%d", w, N, ldy);
-    if (!W || !xq || !xd || !Y) return fail(FA_ERR_INVALID, "%s: null argument", w);
-    if (reinterpret_cast<uintptr_t>(W) % 4 || reinterpret_cast<uintptr_t>(xq) % 16 ||
-        reinterpret_cast<uintptr_t>(xd) % 4 || reinterpret_cast<uintptr_t>(Y) % 2)
-        return fail(FA_ERR_INVALID, "%s: misaligned W (4 B), xq (16 B), xd or Y", w);
-    const long long blocks = (long long)((N + 127) / 128 + 7) / 8 * 8 * ((T + 127) / 128);
-    if (blocks > 0x7fffffffLL) return fail(FA_ERR_UNSUPPORTED, "%s: T=%d x N=%d too large for one launch", w, T, N);
+namespace {
+int gemm_common(const char* w, int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N,
+                uint16_t* Y, int ldy, void* stream, const float* bias, const uint16_t* res, char* ws,
+                const fa::KqPlan& sp) {
     fa::KqGemmParams p{};
     p.W = static_cast<const uint8_t*>(W); p.xq = xq; p.xd = xd; p.Y = Y; p.bias = bias; p.res = res;
     p.row_bytes = friday_q8_row_bytes(kind, K);
     p.T = T; p.K = K; p.N = N; p.ldy = ldy;
-    const fa::KqPlan sp = fa::kq_gemm_plan(T, K, N);
-    int rc = 0;
-    char* ws = static_cast<char*>(gemm_workspace(stream, sp.bytes, &rc));
-    if (rc) return fail(FA_ERR_LAUNCH, "%s: workspace allocation failed", w);
     // no workspace (stream capture without friday_gemm_q8_reserve): one pass over K, and each
     // workgroup dequantises its activation tile itself (the same values)
     if (ws) {
@@ -545,6 +532,51 @@ int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, i
         }
     }
     return launch_status(fa::launch_kq_gemm(kind, p, static_cast<hipStream_t>(stream)), w);
+}
+
+int gemm_check(const char* w, int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N,
+               const uint16_t* Y, int ldy) {
+    if (!friday_gemm_q8_supported(kind, K))
+        return fail(FA_ERR_UNSUPPORTED, "%s: unsupported type %d or K=%d (K must be a multiple of 256)", w, kind, K);
+    if (N <= 0 || ldy < N) return fail(FA_ERR_INVALID, "%s: invalid N=%d / ldy=%d", w, N, ldy);
+    if (!W || !xq || !xd || !Y) return fail(FA_ERR_INVALID, "%s: null argument", w);
+    if (reinterpret_cast<uintptr_t>(W) % 4 || reinterpret_cast<uintptr_t>(xq) % 16 ||
+        reinterpret_cast<uintptr_t>(xd) % 4 || reinterpret_cast<uintptr_t>(Y) % 2)
+        return fail(FA_ERR_INVALID, "%s: misaligned W (4 B), xq (16 B), xd or Y", w);
+    const long long blocks = (long long)((N + 127) / 128 + 7) / 8 * 8 * ((T + 127) / 128);
+    if (blocks > 0x7fffffffLL) return fail(FA_ERR_UNSUPPORTED, "%s: T=%d x N=%d too large for one launch", w, T, N);
+    return FA_OK;
+}
+}  // namespace
+
+int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
+                   int ldy, void* stream, const float* bias, const uint16_t* res) {
+    const char* w = "gemm_q8";
+    if (T <= 0 && friday_gemm_q8_supported(kind, K)) return ok();
+    if (int rc = gemm_check(w, kind, W, xq, xd, T > 0 ? T : 1, K, N, Y, ldy)) return rc;
+    const fa::KqPlan sp = fa::kq_gemm_plan(T, K, N);
+    int rc = 0;
+    char* ws = static_cast<char*>(gemm_workspace(stream, sp.bytes, &rc));
+    if (rc) return fail(FA_ERR_LAUNCH, "%s: workspace allocation failed", w);
+    return gemm_common(w, kind, W, xq, xd, T, K, N, Y, ldy, stream, bias, res, ws, sp);
+}
+
+size_t friday_gemm_q8_workspace_bytes(int T, int K, int N) {
+    if (T <= 0 || N <= 0 || K <= 0 || K % 256) return 0;
+    return fa::kq_gemm_plan(T, K, N).bytes;
+}
+
+int friday_gemm_q8_ws(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
+                      int ldy, void* stream, const float* bias, const uint16_t* res, void* workspace,
+                      size_t workspace_bytes) {
+    const char* w = "gemm_q8_ws";
+    if (T <= 0 && friday_gemm_q8_supported(kind, K)) return ok();
+    if (int rc = gemm_check(w, kind, W, xq, xd, T > 0 ? T : 1, K, N, Y, ldy)) return rc;
+    const fa::KqPlan sp = fa::kq_gemm_plan(T, K, N);
+    if (!workspace || workspace_bytes < sp.bytes || reinterpret_cast<uintptr_t>(workspace) % 256)
+        return fail(FA_ERR_WORKSPACE, "%s: 256-byte aligned workspace of %zu bytes needed (got %zu)", w, sp.bytes,
+                    workspace_bytes);
+    return gemm_common(w, kind, W, xq, xd, T, K, N, Y, ldy, stream, bias, res, static_cast<char*>(workspace), sp);
 }
 
 int friday_gemv_q8(int kind, const void* W, const int8_t* xq, const float* xd, int K, int N, uint16_t* y,

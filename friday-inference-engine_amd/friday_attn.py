@@ -63,6 +63,8 @@ API = [
     ("friday_gemm_q8_supported", _I, [_I, _I]),
     ("friday_gemm_q8", _I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _P]),
     ("friday_gemm_q8_reserve", _I, [_I, _I, _I, _P]),
+    ("friday_gemm_q8_workspace_bytes", _SZ, [_I, _I, _I]),
+    ("friday_gemm_q8_ws", _I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _P, _P, _SZ]),
     ("friday_gemv_q8", _I, [_I, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
 ]
 
@@ -421,6 +423,18 @@ def gemmQ8(kind, W, xq, xd, T, K, N, Y, ldy, stream=None, bias=None, res=None):
 def gemmQ8Reserve(T, K, N, stream=None):
     """Size the K-split workspace of gemmQ8 for (T, K, N) on `stream` before stream capture."""
     _check(load().friday_gemm_q8_reserve(T, K, N, stream))
+
+
+def gemmQ8WorkspaceBytes(T, K, N) -> int:
+    return load().friday_gemm_q8_workspace_bytes(T, K, N)
+
+
+def gemmQ8Ws(kind, W, xq, xd, T, K, N, Y, ldy, workspace, stream=None, bias=None, res=None, workspace_bytes=None):
+    """gemmQ8 with a caller-owned workspace (zeroed once with decodeWorkspaceInit)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
+    _check(load().friday_gemm_q8_ws(kind, _ptr(W), _ptr(xq), _ptr(xd), T, K, N, _ptr(Y), ldy, stream, _ptr(bias),
+                                    _ptr(res), _ptr(workspace), workspace_bytes))
 
 
 def gemvQ8(kind, W, xq, xd, K, N, y, stream=None, W2=None, y2=None, bias=None, res=None):

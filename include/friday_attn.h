@@ -230,7 +230,10 @@ int friday_gemm_q8_supported(int kind, int K);
  * T = 512 with N = 4096, K = 14336), the fp32 partials of a K split, summed in a fixed
  * order so that results do not depend on timing. Under stream capture the workspace is not
  * allocated: a call then dequantises per workgroup and runs unsplit (same values, slower)
- * unless friday_gemm_q8_reserve sized it beforehand. */
+ * unless friday_gemm_q8_reserve sized it beforehand. Calls on one stream share its
+ * workspace in stream order: a graph that contains friday_gemm_q8 must be replayed on the
+ * stream it was captured on, and never concurrently with another replay or call that uses
+ * that stream's workspace (friday_gemm_q8_ws with a workspace per graph has no such rule). */
 int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
                    int ldy, void* stream, const float* bias, const uint16_t* res);
 /* No counterpart in the reference (its GEMM needs no workspace; cf. ensureQ8Scratch,
@@ -238,6 +241,16 @@ int friday_gemm_q8(int kind, const void* W, const int8_t* xq, const float* xd, i
  * `stream` ahead of stream capture. FA_ERR_WORKSPACE when called during capture and an
  * allocation would be needed. */
 int friday_gemm_q8_reserve(int T, int K, int N, void* stream);
+/* No counterpart in the reference: friday_gemm_q8 with a caller-owned workspace, so that
+ * each captured graph (or each concurrent stream) can have its own. Size it with
+ * friday_gemm_q8_workspace_bytes (0 for invalid shapes), align it to 256 bytes and zero it
+ * once with friday_attn_decode_workspace_init before first use; every call leaves its
+ * split counters at zero again. Calls that share one workspace must not overlap.
+ * FA_ERR_WORKSPACE if it is missing, misaligned or too small. */
+size_t friday_gemm_q8_workspace_bytes(int T, int K, int N);
+int friday_gemm_q8_ws(int kind, const void* W, const int8_t* xq, const float* xd, int T, int K, int N, uint16_t* Y,
+                      int ldy, void* stream, const float* bias, const uint16_t* res, void* workspace,
+                      size_t workspace_bytes);
 /* Replaces friday_hpc::gemvQ8 (hpc_k_quants.h:64-68, hpc_k_quants.cu:904-931), the decode
  * GEMV with int8 activations (the O-projection after attention, transformer.cpp:1057-1059):
  * y[n] = sum_k W[n][k] x[k] for one vector x given as xq [K] int8 and xd [K/32] fp32 (the

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <stdexcept>
+#include <vector>
 #include <string>
 
 #include "friday_attn.h"
@@ -114,6 +115,7 @@ struct Q8Scratch {
     int8_t* xq = nullptr;
     float* xd = nullptr;
     int cap = 0;
+    std::vector<void*> retired;  // outgrown buffers: a captured graph may still use them
 };
 inline Q8Scratch& scratch() {
     static Q8Scratch s;
@@ -121,13 +123,21 @@ inline Q8Scratch& scratch() {
 }
 }  // namespace detail
 
-// The activation scratch shared by quantizeQ8 and gemvQ8 (hpc_k_quants.h:51-57): allocate
-// it for vectors of up to K values before any HIP graph capture.
-inline void ensureQ8Scratch(int K, hipStream_t) {
+// The activation scratch shared by quantizeQ8 and gemvQ8 (hpc_k_quants.h:51-57, the
+// reference's ensureQ8Scratch at hpc_k_quants.cu:869-878): allocate it for vectors of up to
+// K values before any HIP graph capture. Growing it during a capture throws. The buffers it
+// outgrows are not freed (graphs captured earlier keep using them) until the process ends.
+inline void ensureQ8Scratch(int K, hipStream_t stream) {
     auto& s = detail::scratch();
     if (K <= s.cap) return;
-    if (s.xq) (void)hipFree(s.xq);
-    if (s.xd) (void)hipFree(s.xd);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        throw std::runtime_error("ensureQ8Scratch: cannot grow the scratch during stream capture");
+    if (s.xq) s.retired.push_back(s.xq);
+    if (s.xd) s.retired.push_back(s.xd);
+    s.xq = nullptr;
+    s.xd = nullptr;
+    s.cap = 0;
     const int cap = (K + 255) / 256 * 256;
     if (hipMalloc(reinterpret_cast<void**>(&s.xq), (size_t)cap) != hipSuccess ||
         hipMalloc(reinterpret_cast<void**>(&s.xd), (size_t)cap / 32 * sizeof(float)) != hipSuccess)

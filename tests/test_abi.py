@@ -172,6 +172,17 @@ def test_gemm_q8_validation(fa):
     assert L.friday_gemm_q8_reserve(0, 4096, 64, None) == fa.FA_ERR_INVALID
     assert L.friday_gemm_q8_reserve(4, 4000, 64, None) == fa.FA_ERR_INVALID
     assert L.friday_gemm_q8_reserve(4, 4096, -1, None) == fa.FA_ERR_INVALID
+    # caller-owned workspace: sized by friday_gemm_q8_workspace_bytes, missing / small / misaligned rejected
+    assert L.friday_gemm_q8_workspace_bytes(0, 4096, 64) == 0
+    assert L.friday_gemm_q8_workspace_bytes(4, 4000, 64) == 0
+    need = L.friday_gemm_q8_workspace_bytes(512, 14336, 4096)
+    assert need > L.friday_gemm_q8_workspace_bytes(512, 4096, 4096) > 0
+    args = (fa.Q4_K, FAKE, FAKE, FAKE, 512, 14336, 4096, FAKE, 4096, None, None, None)
+    assert L.friday_gemm_q8_ws(*args, None, need) == fa.FA_ERR_WORKSPACE
+    assert L.friday_gemm_q8_ws(*args, FAKE, need - 1) == fa.FA_ERR_WORKSPACE
+    assert L.friday_gemm_q8_ws(*args, FAKE + 16, need) == fa.FA_ERR_WORKSPACE
+    assert "workspace" in err(fa)
+    assert L.friday_gemm_q8_ws(fa.Q4_K, FAKE, FAKE, FAKE, 0, 256, 64, FAKE, 64, None, None, None, None, 0) == fa.FA_OK
     # activation quantiser: K multiple of 32
     assert L.friday_quantize_q8_rows(FAKE, 2, 48, FAKE, FAKE, None) == fa.FA_ERR_INVALID
     assert L.friday_quantize_q8_rows(FAKE, 0, 64, FAKE, FAKE, None) == fa.FA_OK

@@ -240,6 +240,41 @@ def test_split_k_graph_replay(gpu, oracle):
                               f"graph reserve={reserve}")
 
 
+def test_caller_workspace_graphs(gpu):
+    """friday_gemm_q8_ws: two graphs, each with its own workspace, captured on one stream and
+    replayed alternately on two other streams, give the library-workspace call's bits on
+    every replay (split K, 512 x 14336 -> 4096 as the 8B ffn_down)."""
+    fa = gpu
+    rng = np.random.default_rng(7)
+    kind, T, K, N = 5, 512, 14336, 4096
+    W = fa.DeviceBuffer.from_array(kq_random_weights(rng, kind, N, K))
+    x = rng.standard_normal((T, K), dtype=np.float32).astype(np.float16).view(np.uint16)
+    dq, dd = fa.DeviceBuffer(T * K), fa.DeviceBuffer(T * K // 32 * 4)
+    fa.quantizeQ8Rows(fa.DeviceBuffer.from_array(x), T, K, dq, dd)
+    ref = fa.DeviceBuffer(T * N * 2)
+    fa.gemmQ8(kind, W, dq, dd, T, K, N, ref, N)
+    fa.Hip.sync()
+    ref_bits = ref.download((T, N), np.uint16)
+    nbytes = fa.gemmQ8WorkspaceBytes(T, K, N)
+    cap = fa.Stream()
+    graphs, outs = [], []
+    for _ in range(2):
+        ws = fa.DeviceBuffer(nbytes)
+        fa.decodeWorkspaceInit(ws)
+        fa.Hip.sync()
+        y = fa.DeviceBuffer(T * N * 2)
+        graphs.append(fa.Graph(cap, lambda ws=ws, y=y: fa.gemmQ8Ws(kind, W, dq, dd, T, K, N, y, N, ws, stream=cap.s)))
+        outs.append((y, ws))
+    runs = [fa.Stream(), fa.Stream()]
+    for rep in range(3):
+        for i, g in enumerate(graphs):
+            outs[i][0].fill_bytes(0)
+            fa.Hip.lib().hipGraphLaunch(g.exec, runs[(i + rep) % 2].s)
+        fa.Hip.sync()
+        for i in range(2):
+            assert np.array_equal(outs[i][0].download((T, N), np.uint16), ref_bits), f"graph {i} replay {rep}"
+
+
 @pytest.mark.parametrize("T,K,N,kind", [(130, 768, 96, 4), (37, 1024, 200, 1), (300, 1024, 2100, 6)])
 def test_prehoisted_activations_bit_identical(gpu, T, K, N, kind):
     """The eager call dequantises the activations once into the workspace (fp16) and stages
