@@ -84,6 +84,14 @@ __device__ __forceinline__ float col_max4(float v) {
 }
 __device__ __forceinline__ float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 
+// sum of v over the lanes l, l^16, l^32, l^48, the same bits in all four lanes
+__device__ __forceinline__ float col_sum4(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Agent-scope coherent access (global_store/load ... sc1): the store is written
 // through to the device coherence point and the load bypasses a possibly stale
 // XCD-local L2 line, so data handed between workgroups of one launch needs no

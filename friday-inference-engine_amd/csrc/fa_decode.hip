@@ -28,16 +28,11 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTile = 16;  // positions per wave tile
-#ifndef FA_DECODE_STAGES
-#define FA_DECODE_STAGES 1
-#endif
-constexpr int kStages = FA_DECODE_STAGES;  // register stages (tiles in flight) per wave
-#ifndef FA_DECODE_STAGES_Q8
-#define FA_DECODE_STAGES_Q8 2
-#endif
+constexpr int kStages = 1;    // register stages (tiles in flight) per wave
 // int8 rows are half as wide: twice the tiles in flight keep the same bytes in flight
-constexpr int kStagesQ8 = FA_DECODE_STAGES_Q8;
-constexpr int kShortStages = 4;            // stages when a wave has at most this many tiles
+constexpr int kStagesQ8 = 2;
+constexpr int kShortStages = 4;
+constexpr int kMergeSlices = 8;  // column slices of the distributed fused merge            // stages when a wave has at most this many tiles
 
 template <int D, bool Q8>
 struct Geo {
@@ -52,9 +47,7 @@ struct Geo {
     static constexpr int WAVE_LDS = 2 * kTile * LROW;  // K and V tile of one wave
     static constexpr int CROW = D + 4;                 // combine row stride in floats (bank spread)
     static constexpr int COMB_LDS = (2 * kWaves * 16 + kWaves * 16 * CROW) * 4;
-    static constexpr int MERGE_LDS = (2 * (kThreads / (D / 4)) * 128 + 64) * 4;
-    static constexpr int LDS0 = (kWaves * WAVE_LDS > COMB_LDS ? kWaves * WAVE_LDS : COMB_LDS);
-    static constexpr int LDS = LDS0 > MERGE_LDS ? LDS0 : MERGE_LDS;
+    static constexpr int LDS = kWaves * WAVE_LDS + COMB_LDS;  // tiles, then the wave combine
 };
 
 __device__ __forceinline__ int context_len(const DecodeParams& p, int b, bool paged) {
@@ -115,8 +108,9 @@ __device__ __forceinline__ void quant_chunk16(const h8* x, u4& q, float& scale, 
 // caller asked for it, their int8 form: per 32 values d = amax / 127, q = clamp(rne(x / d)),
 // exactly as quantize_x_q8_kernel (hpc_k_quants.cu:386-400) applied to the fp16 output.
 // The 8 lanes holding one 32-value block (consecutive c, same row) must call it together.
-__device__ __forceinline__ void store_out4(const DecodeParams& p, size_t row, int D, int c, h4 o) {
-    reinterpret_cast<h4*>(p.out + row * D)[c] = o;
+__device__ __forceinline__ void store_out4(const DecodeParams& p, size_t row, int D, int c, h4 o, bool st = true,
+                                           int lstride = 1) {
+    if (st) reinterpret_cast<h4*>(p.out + row * D)[c] = o;
     if (p.out_q) {
         float v[4], amax = 0.0f;
 #pragma unroll
@@ -125,7 +119,7 @@ __device__ __forceinline__ void store_out4(const DecodeParams& p, size_t row, in
             amax = fmaxf(amax, fabsf(v[i]));
         }
 #pragma unroll
-        for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 8));
+        for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off * lstride, 64));
         const float d = amax / 127.0f;
         const float inv = d > 0.0f ? 1.0f / d : 0.0f;
         uint32_t packed = 0;
@@ -135,193 +129,138 @@ __device__ __forceinline__ void store_out4(const DecodeParams& p, size_t row, in
             q = q < -127 ? -127 : (q > 127 ? 127 : q);
             packed |= (uint32_t)(q & 0xFF) << (8 * i);
         }
-        *reinterpret_cast<uint32_t*>(p.out_q + row * D + 4 * c) = packed;
-        if ((c & 7) == 0) p.out_d[(row * D + 4 * c) / 32] = d;
+        if (st) {
+            *reinterpret_cast<uint32_t*>(p.out_q + row * D + 4 * c) = packed;
+            if ((c & 7) == 0) p.out_d[(row * D + 4 * c) / 32] = d;
+        }
     }
 }
 
-template <int D, int NB>
-__device__ void merge_heads(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
-    constexpr int C4 = D / 4;
-    constexpr int HB = kThreads / C4;  // heads per pass
-    constexpr int K = kMaxSplitsLimit;
-    float* s_m = lds;            // [HB][K]  max of each split, then its weight
-    float* s_l = s_m + HB * K;   // [HB][K]  sum of each split, then weight * sum
-    const int tid = threadIdx.x;
-    const int hh = tid / C4, c = tid % C4;
-    const int npad = (nsp + 7) & ~7;  // padded entries: max -inf, sum 0 -> weight exactly 0
-    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(p.part_o + row0 * p.nsplit_grid * D, (uint32_t)(nh * p.nsplit_grid * D * 4));
-    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml + row0 * p.nsplit_grid * 2, (uint32_t)(nh * p.nsplit_grid * 8));
-    for (int h0 = 0; h0 < nh; h0 += HB) {
-        const int hn = min(HB, nh - h0);
-        const bool act = hh < hn;
-        const size_t orow = row0 + h0 + (act ? hh : 0);
-        const uint32_t obase = (uint32_t)(((h0 + (act ? hh : 0)) * p.nsplit_grid * D + 4 * c) * 4);
-        // (max, sum) of every split first: the weights need them before anything else
-        constexpr int NR = (HB * K + kThreads - 1) / kThreads;
-        float2 mlv[NR];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            // unconditional (clamped) loads: a branch here would drain the load counter
-            // before the partial-O loads below are issued
-            const int i = min(tid + r * kThreads, hn * npad - 1);
-            const int h = i / npad, sp = i - h * npad;
-            mlv[r] = ld_coherent2(rml, (uint32_t)(((h0 + h) * p.nsplit_grid + min(sp, nsp - 1)) * 8));
-        }
-        // then this thread's partial columns, in flight while the weights are computed
-        f4 ov[NB];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int i = tid + r * kThreads;
-            if (i < hn * npad) {
-                const int h = i / npad, sp = i - h * npad;
-                s_m[h * K + sp] = sp < nsp ? mlv[r].x : -__builtin_inff();
-                s_l[h * K + sp] = sp < nsp ? mlv[r].y : 0.0f;
-            }
-        }
-        __syncthreads();
-        // one thread per (head, split): the head's max, then this split's weight
-        float wgt[NR], wl[NR];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int i = tid + r * kThreads;
-            wgt[r] = 0.0f;
-            wl[r] = 0.0f;
-            if (i < hn * npad) {
-                const int h = i / npad, sp = i - h * npad;
-                const float* m = s_m + h * K;
-                float M = -__builtin_inff();
-                for (int t = 0; t < npad; t += 8)
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) M = fmaxf(M, m[t + k]);
-                const float df = m[sp] - M;
-                wgt[r] = df < kCut2 ? 0.0f : exp2_fast(df);
-                wl[r] = wgt[r] * s_l[h * K + sp];
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int i = tid + r * kThreads;
-            if (i < hn * npad) {
-                const int h = i / npad, sp = i - h * npad;
-                s_m[h * K + sp] = wgt[r];
-                s_l[h * K + sp] = wl[r];
-            }
-        }
-        __syncthreads();
-        if (act) {
-            // L in a fixed order (eight interleaved partial sums, then a tree), the same in
-            // every thread of the head
-            const float* wlh = s_l + hh * K;
-            float Lp[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) Lp[k] = 0.0f;
-            for (int t = 0; t < npad; t += 8)
-#pragma unroll
-                for (int k = 0; k < 8; ++k) Lp[k] += wlh[t + k];
-            const float L = ((Lp[0] + Lp[1]) + (Lp[2] + Lp[3])) + ((Lp[4] + Lp[5]) + (Lp[6] + Lp[7]));
-            const float* w = s_m + hh * K;
-            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < NB; ++j)
-                if (j < nsp) acc += w[j] * ov[j];
-            for (int sp = NB; sp < nsp; ++sp) acc += w[sp] * ld_coherent4(ro, obase + (uint32_t)(sp * D * 4));
-            h4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
-            store_out4(p, orow, D, c, o);
-        }
-        __syncthreads();  // LDS reused by the next pass
-    }
+// Cross-lane steps within groups of 8 lanes by DPP (no LDS round trip): lane ^ 1, lane ^ 2
+// (quad permutations) and lane 7 - i of its group (half-row mirror).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror8 = 0x141;
+// Sum over the 8 lanes of a group by the tree ((0+1)+(2+3))+((4+5)+(6+7)) in every lane
+// (float addition is commutative, so all 8 lanes hold the same bits).
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    return v + dpp<kDppMirror8>(v);
+}
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    return fmaxf(v, dpp<kDppMirror8>(v));
 }
 
-// The same merge for nsp <= NB, with no per-split branch or dependent LDS chain:
-// the (max, sum) table of a head is padded to NB entries (max -inf, sum 0, so the
-// weight is exactly 0), and every output thread reads its head's table with vector
-// LDS loads and computes the head's max and weights itself. The arithmetic and its
-// order are those of merge_heads, so both give the same bits.
-template <int D, int NB>
-__device__ void merge_short(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
-    constexpr int C4 = D / 4;
-    constexpr int HB = kThreads / C4;  // heads per pass
-    constexpr int NE = HB * NB;        // table entries per pass
-    constexpr int NR = (NE + kThreads - 1) / kThreads;  // table entries per thread
-    float* s_m = lds;        // [HB][NB]
-    float* s_l = s_m + NE;   // [HB][NB]
-    const int tid = threadIdx.x;
-    const int hh = tid / C4, c = tid % C4;
-    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(p.part_o + row0 * p.nsplit_grid * D, (uint32_t)(nh * p.nsplit_grid * D * 4));
-    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml + row0 * p.nsplit_grid * 2, (uint32_t)(nh * p.nsplit_grid * 8));
-    for (int h0 = 0; h0 < nh; h0 += HB) {
-        const int hn = min(HB, nh - h0);
-        const bool act = hh < hn;
-        const uint32_t obase = (uint32_t)(((h0 + (act ? hh : 0)) * p.nsplit_grid * D + 4 * c) * 4);
-        // this thread's table entries, then its partial columns: one memory round trip
-        float2 mlv[NR];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int ei = min(tid + r * kThreads, hn * NB - 1);
-            mlv[r] = ld_coherent2(rml, (uint32_t)(((h0 + ei / NB) * p.nsplit_grid + min(ei % NB, nsp - 1)) * 8));
-        }
-        f4 ov[NB];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) ov[j] = ld_coherent4(ro, obase + (uint32_t)(min(j, nsp - 1) * D * 4));
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int e = tid + r * kThreads;
-            if (e < NE) {
-                const bool live = e < hn * NB && e % NB < nsp;
-                s_m[e] = live ? mlv[r].x : -__builtin_inff();
-                s_l[e] = live ? mlv[r].y : 0.0f;
-            }
-        }
-        __syncthreads();
-        if (act) {
-            float m[NB], l[NB];
-#pragma unroll
-            for (int j = 0; j < NB; j += 4) {
-                *reinterpret_cast<f4*>(m + j) = *reinterpret_cast<const f4*>(s_m + hh * NB + j);
-                *reinterpret_cast<f4*>(l + j) = *reinterpret_cast<const f4*>(s_l + hh * NB + j);
-            }
-            float M = -__builtin_inff();
-#pragma unroll
-            for (int j = 0; j < NB; ++j) M = fmaxf(M, m[j]);
-            float Lp[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) Lp[k] = 0.0f;
-            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const float df = m[j] - M;
-                const float w = df < kCut2 ? 0.0f : exp2_fast(df);
-                Lp[j % 8] += w * l[j];
-                acc += w * ov[j];
-            }
-            const float L = ((Lp[0] + Lp[1]) + (Lp[2] + Lp[3])) + ((Lp[4] + Lp[5]) + (Lp[6] + Lp[7]));
-            h4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = out_half(L > 1e-12f ? acc[i] / L : 0.0f);
-            store_out4(p, row0 + h0 + hh, D, c, o);
-        }
-        if (h0 + HB < nh) __syncthreads();  // LDS reused by the next pass
-    }
-}
-
+// Log-sum-exp merge of the split partials (attention_kernels.cu:207-235) over the output
+// columns [4 c0, 4 (c0 + cw)) of nh consecutive head rows row0 ..: per (head, column)
+//   M = max_s m_s; w_s = exp(m_s - M) (0 below -50); lane r of the unit's 8 lanes sums
+//   L_r = sum w_s l_s and acc_r = sum w_s o_s over s = r, r + 8, ... in increasing order;
+//   L and acc are the sums of the 8 lane values by the fixed tree of sum8;
+//   out = L > 1e-12 ? acc * (1 / L) : 0, NaN -> 0, clamp, fp16.
+// Eight lanes serve one (head, float4 column) unit straight from memory (sc1 loads,
+// coherent with the sc1 stores of the other workgroups): up to 32 splits cost each lane
+// 4 + 4 loads in one round trip, with no LDS and no barrier. The order of the arithmetic
+// does not depend on the column range or on which workgroup runs it, so the separate
+// merge kernel and the column slices of the fused merge give the same bits. cw must be a
+// power of two; with out_q, cw and c0 must be multiples of 8.
 template <int D>
-__device__ __forceinline__ void merge_any(const DecodeParams& p, size_t row0, int nh, int nsp, float* lds) {
-    if (nsp <= 8)
-        merge_short<D, 8>(p, row0, nh, nsp, lds);
-    else if (nsp <= 32)
-        merge_short<D, 32>(p, row0, nh, nsp, lds);
-    else
-        merge_heads<D, 32>(p, row0, nh, nsp, lds);
+__device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, int c0, int cw) {
+    const int tid = threadIdx.x, r = tid & 7;
+    const int wunit = __builtin_amdgcn_readfirstlane(tid >> 6) * 8;  // first unit of this wave in a pass
+    const uint32_t ng = (uint32_t)p.nsplit_grid;
+    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(p.part_o, 0x7fffffff);
+    const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml, 0x7fffffff);
+    const int lc = __builtin_ctz(cw);
+    const int units = nh * cw;
+    for (int u0 = 0; u0 < units; u0 += kThreads / 8) {
+        if (u0 + wunit >= units) break;  // uniform: no unit left for this wave
+        const int uu = u0 + (tid >> 3);
+        const int u = min(uu, units - 1);  // lanes past the last unit repeat it
+        const int hh = u >> lc, c = c0 + (u & (cw - 1));
+        const uint32_t row = (uint32_t)(row0 + hh) * ng;
+        // splits r, r + 8, r + 16, r + 24 (all of them up to 32 splits) in one round trip
+        float2 ml[4];
+        f4 ov[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = (uint32_t)min(r + 8 * i, nsp - 1);
+            ml[i] = ld_coherent2(rml, (row + j) * 8);
+            ov[i] = ld_coherent4(ro, ((row + j) * D + 4 * (uint32_t)c) * 4);
+        }
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) M = fmaxf(M, r + 8 * i < nsp ? ml[i].x : -__builtin_inff());
+        for (int j0 = r + 32; j0 < nsp; j0 += 8)  // beyond 32 splits
+            M = fmaxf(M, ld_coherent2(rml, (row + (uint32_t)j0) * 8).x);
+        M = max8(M);
+        float L = 0.0f;
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float df = (r + 8 * i < nsp ? ml[i].x : -__builtin_inff()) - M;
+            const float w = df < kCut2 ? 0.0f : exp2_fast(df);
+            L += w * (r + 8 * i < nsp ? ml[i].y : 0.0f);
+            acc += w * ov[i];
+        }
+        for (int j0 = r + 32; j0 < nsp; j0 += 8) {
+            const float2 m2 = ld_coherent2(rml, (row + (uint32_t)j0) * 8);
+            const f4 o2 = ld_coherent4(ro, ((row + (uint32_t)j0) * D + 4 * (uint32_t)c) * 4);
+            const float df = m2.x - M;
+            const float w = df < kCut2 ? 0.0f : exp2_fast(df);
+            L += w * m2.y;
+            acc += w * o2;
+        }
+        L = sum8(L);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = sum8(acc[i]);
+        const float inv = L > 1e-12f ? 1.0f / L : 0.0f;
+        h4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = out_half(acc[i] * inv);
+        store_out4(p, row0 + hh, D, c, o, uu < units && r == 0, 8);
+    }
 }
 
+// Whole-row merge of nh head rows.
 template <int D>
-constexpr int merge_lds_bytes() { return (2 * (kThreads / (D / 4)) * kMaxSplitsLimit + 64) * 4; }
+__device__ __forceinline__ void merge_any(const DecodeParams& p, size_t row0, int nh, int nsp) {
+    merge_cols<D>(p, row0, nh, nsp, 0, D / 4);
+}
+
+// Column slice k of nslice of the fused merge.
+template <int D>
+__device__ __forceinline__ void merge_slice(const DecodeParams& p, size_t row0, int nh, int nsp, int k, int nslice) {
+    const int cw = (D / 4) / nslice;
+    merge_cols<D>(p, row0, nh, nsp, k * cw, cw);
+}
+
+// Number of column slices the fused merge of a group is spread over: the launcher's
+// choice (kMergeSlices), at most nsp, a divisor
+// of the D/4 float4 columns, and with out_q at least 8 columns (whole 32-value
+// blocks) per slice.
+template <int D>
+__device__ __forceinline__ int merge_slices(const DecodeParams& p, int nsp) {
+    int n = p.merge_slices;
+    while (n > 1 && (n > nsp || (p.out_q && (D / 4) / n < 8))) n >>= 1;
+    return n;
+}
+
+// Wait of one thread until the arrival counter reaches `target` (unsigned, wrapping). The
+// workgroups it waits for were dispatched before the waiting one, so the wait ends; it is
+// still bounded (kSpinTicks of the 100 MHz real-time clock), after which the merge goes
+// ahead with whatever partials are there.
+constexpr uint64_t kSpinTicks = 100000000;  // 1 s
+__device__ __forceinline__ void wait_count(const unsigned* cnt, unsigned target) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while ((int)(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) return;
+    }
+}
 
 template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
 // two workgroups per CU (two waves per SIMD) must fit: a 256-register budget
@@ -341,6 +280,14 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
                                : split_chunk(S, p.min_chunk, p.max_splits);
     const int nsp = p.single ? 1 : split_count(S, p.min_chunk, p.max_splits);
     if (split >= nsp) return;  // inactive split; the merge ignores it
+    // fused merge (see the end of the kernel): this workgroup's merge slice (mk >= 0 for the
+    // last nslice splits) and, for mergers, the group's counter base, loaded early
+    const int nslice = (nsp > 1 && p.counters) ? merge_slices<D>(p, nsp) : 1;
+    const int mk = split - (nsp - nslice);
+    unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * kCounterStride;
+    unsigned base = 0;
+    if (nsp > 1 && p.counters && mk >= 0)
+        base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
 
@@ -530,14 +477,20 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         float ks[Gm::NLD], vs[Gm::NLD];
     };
 
+    // A tile past the end (the refill after a wave's last tile) reads this workgroup's q row
+    // instead: valid memory that is already cached, so its loads are cheap to wait for.
+    const char* qrow_bytes = reinterpret_cast<const char*>(p.q + (size_t)b * p.Hq * D + (size_t)kvh * p.G * D);
     auto load_tile = [&](Stage& st, int t) {
         const int base = start + t * kTile;
+        const bool past = t >= ntiles;  // uniform
+        const char* kb = past ? qrow_bytes : kbase;
+        const char* vb = past ? qrow_bytes : vbase;
 #pragma unroll
         for (int r = 0; r < Gm::NLD; ++r) {
             const int pos = base + r * Gm::RPI + lrow;
-            const size_t ri = row_index<PAGED>(p, b, max(min(pos, end - 1), start));
-            st.k[r] = ld_nt(reinterpret_cast<const u4*>(kbase + ri * rowb) + lchunk);
-            st.v[r] = ld_nt(reinterpret_cast<const u4*>(vbase + ri * rowb) + lchunk);
+            const size_t ri = past ? 0 : row_index<PAGED>(p, b, max(min(pos, end - 1), start));
+            st.k[r] = ld_nt(reinterpret_cast<const u4*>(kb + ri * rowb) + lchunk);
+            st.v[r] = ld_nt(reinterpret_cast<const u4*>(vb + ri * rowb) + lchunk);
             if (Q8) {
                 const size_t si = (ri * p.kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
                 st.ks[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
@@ -582,8 +535,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         }
         // LDS operations of one wave complete in order: the reads below see these writes.
         __builtin_amdgcn_wave_barrier();
-        // Refill this stage while computing. Unconditional (a tile past the end re-reads
-        // the split's last row, an L2 hit) so no branch hides loads from the wait counter.
+        // Refill this stage while computing. Unconditional, so no branch hides loads from the
+        // wait counter: a tile past the end reads this wave's q row instead (L1-resident).
         load_tile(st, t_next);
         if (t >= ntiles) return;  // uniform: this stage held no tile
 
@@ -657,10 +610,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         stream(std::integral_constant<int, NST>{});
 
     // ---- combine the four waves of the workgroup through LDS ----
-    l_run = wave_sum_xor(l_run, 16);
-    l_run = wave_sum_xor(l_run, 32);
-    __syncthreads();  // all waves done with their tiles; LDS is reused
-    float* cm = reinterpret_cast<float*>(smem);           // [kWaves][16]
+    // (each wave writes its state into a region of its own, so no barrier is needed before)
+    l_run = col_sum4(l_run);
+    float* cm = reinterpret_cast<float*>(smem + kWaves * Gm::WAVE_LDS);  // [kWaves][16]
     float* cl = cm + kWaves * 16;                          // [kWaves][16]
     float* co = cl + kWaves * 16;                          // [kWaves][16][CROW]
     if (kb == 0) {
@@ -715,24 +667,28 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     };
     if (nsp == 1) write_q();
 
-    // Fused merge: the last workgroup of this (sequence, kv head, head block) to
-    // arrive merges the partials of its query heads and re-arms the counter.
+    // Fused merge. Every workgroup of this (sequence, kv head, head block) adds 1 to the
+    // group's arrival counter once its partials are stored, and does not wait for the
+    // atomic. The counter is never reset: a launch is complete when it has grown by nsp
+    // over the group's base, which merger 0 then advances by nsp for the next launch.
+    // The mergers are the last nslice splits of the group, i.e. the workgroups dispatched
+    // last (workgroups are dispatched in increasing id order): each waits until the
+    // counter is complete, which only needs workgroups dispatched before it, then merges
+    // its column slice. Merger 0 also writes the rotated q back and advances the base.
     if (nsp > 1 && p.counters) {
-        __shared__ int s_last;
         // The partials were written through to the device coherence point (sc1 stores);
         // wait until every one of them has completed before this workgroup is counted.
         wait_vmem();
         __syncthreads();
-        if (tid == 0) {
-            int* cnt = p.counters + ((size_t)b * gridDim.x + group) * kCounterStride;
-            const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = prev == nsp - 1;
-            if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (mk < 0) return;
+        if (tid == 0) wait_count(cnt, base + (unsigned)nsp);
         __syncthreads();
-        if (s_last) {
-            merge_any<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, reinterpret_cast<float*>(smem));
+        merge_slice<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
+        if (mk == 0) {
             write_q();  // every workgroup of the group has read q by now
+            if (tid == 0) __hip_atomic_store(cnt + kCounterStride / 2, base + (unsigned)nsp, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -740,17 +696,18 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
 // Second pass of the two-kernel path: one workgroup per (sequence, head).
 template <int D, bool PAGED>
 __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
-    __shared__ __align__(16) float lds[merge_lds_bytes<D>() / 4];
     const int row = blockIdx.x;  // b * Hq + head
     const int S = context_len(p, row / p.Hq, PAGED);
     const int nsp = split_count(S, p.min_chunk, p.max_splits);
     if (p.single || nsp <= 1) return;  // the decode kernel wrote the output
-    merge_any<D>(p, (size_t)row, 1, nsp, lds);
+    merge_any<D>(p, (size_t)row, 1, nsp);
 }
 
 template <int D, bool PAGED, bool Q8>
-int launch_t(const DecodeParams& p, int batch, hipStream_t stream) {
+int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
+    DecodeParams p = p_in;
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
+    p.merge_slices = kMergeSlices;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
         hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid, dim3(kThreads), 0, stream, p);
