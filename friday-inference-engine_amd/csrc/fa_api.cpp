@@ -311,6 +311,62 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
                               num_heads, num_kv_heads, head_dim, rope_table, neox, workspace, workspace_bytes, stream);
 }
 
+namespace {
+// Device scratch of friday_attn_decode_step_noalloc: the arrival counters and split
+// partials that a caller's workspace holds otherwise. 4 MiB covers up to 4096 query heads
+// at d <= 128: at most 4096 partial rows of d + 2 floats (2.1 MB) plus one 256-byte
+// counter slot per head (1 MB). Every GPU the
+// library runs on holds its own copy until the process ends.
+constexpr size_t kScratchBytes = size_t(4) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[64];
+
+// The device address of the current device's scratch (the host-side name `scratch` is not
+// one), looked up once per device; the first call also zeroes it with a fill kernel on
+// `stream` (the counters must start at zero; every call leaves them at zero).
+void* scratch_ptr(hipStream_t stream, hipError_t* err) {
+    int dev = 0;
+    if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
+    if (dev < 0 || dev >= 64) return *err = hipErrorInvalidDevice, nullptr;
+    ScratchSlot& s = g_scratch[dev];
+    std::call_once(s.once, [&] {
+        void* ptr = nullptr;
+        s.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (s.err == hipSuccess && fa::launch_zero_fill(ptr, kScratchBytes, stream) != 0) s.err = hipGetLastError();
+        if (s.err == hipSuccess) s.ptr = ptr;
+    });
+    *err = s.err;
+    return s.ptr;
+}
+}  // namespace
+
+int friday_attn_decode_step_noalloc(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer,
+                                    uint16_t* v_layer, uint16_t* out, const int* d_pos, int pos, int max_ctx,
+                                    int num_heads, int num_kv_heads, int head_dim, const float* rope_table, int neox,
+                                    void* stream) {
+    const char* w = "decode_step_noalloc";
+    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
+    if (!q || !k || !v || !k_layer || !v_layer || !out || !rope_table || max_ctx <= 0)
+        return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if (!d_pos && (pos < 0 || pos >= max_ctx))
+        return fail(FA_ERR_INVALID, "%s: position %d outside [0, %d)", w, pos, max_ctx);
+    const size_t need = split_ws_bytes(1, num_heads, d_pos ? max_ctx : pos + 1, head_dim);
+    if (need > kScratchBytes)
+        return fail(FA_ERR_WORKSPACE, "%s: needs %zu bytes of scratch, more than the %zu held per GPU", w, need,
+                    kScratchBytes);
+    hipError_t err = hipSuccess;
+    void* ws = scratch_ptr(static_cast<hipStream_t>(stream), &err);
+    if (!ws) return fail(FA_ERR_LAUNCH, "%s: device scratch unavailable: %s", w, hipGetErrorString(err));
+    return decode_step_common(w, q, k, v, k_layer, v_layer, nullptr, nullptr, out, d_pos, pos, max_ctx, num_heads,
+                              num_kv_heads, head_dim, rope_table, neox, ws, kScratchBytes, stream);
+}
+
 int friday_attn_decode_step_q8(uint16_t* q, const uint16_t* k, const uint16_t* v, int8_t* k_layer,
                                uint16_t* k_scale, int8_t* v_layer, uint16_t* v_scale, uint16_t* out,
                                const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads,

@@ -46,6 +46,7 @@ API = [
     ("friday_attn_decode_workspace_init", _I, [_P, _SZ, _P]),
     ("friday_attn_decode_attention_fused", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     ("friday_attn_decode_step", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
+    ("friday_attn_decode_step_noalloc", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
     ("friday_attn_decode_step_q8", _I,
      [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_prefill_supported", _I, [_I, _I, _I]),
@@ -341,6 +342,14 @@ def decodeStep(q, k, v, k_layer, v_layer, out, d_pos, pos, max_ctx, num_heads, n
     _check(load().friday_attn_decode_step(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(v_layer), _ptr(out),
                                           _ptr(d_pos), pos, max_ctx, num_heads, num_kv_heads, head_dim,
                                           _ptr(rope_table), int(neox), _ptr(workspace), workspace_bytes, stream))
+
+
+def decodeStepNoAlloc(q, k, v, k_layer, v_layer, out, d_pos, pos, max_ctx, num_heads, num_kv_heads, head_dim,
+                      rope_table, neox, stream=None):
+    """decodeStep on the library's per-GPU device scratch: no workspace, no allocation."""
+    _check(load().friday_attn_decode_step_noalloc(_ptr(q), _ptr(k), _ptr(v), _ptr(k_layer), _ptr(v_layer), _ptr(out),
+                                                  _ptr(d_pos), pos, max_ctx, num_heads, num_kv_heads, head_dim,
+                                                  _ptr(rope_table), int(neox), stream))
 
 
 def decodeStepQ8(q, k, v, k_layer, k_scale, v_layer, v_scale, out, d_pos, pos, max_ctx, num_heads, num_kv_heads,
