@@ -127,6 +127,13 @@ __device__ __forceinline__ void st_coherent2(__amdgpu_buffer_rsrc_t r, uint32_t 
     __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const i2v*>(&v), r, (int)byte_off, 0, kCpolSc1);
 }
 
+// Materialises a wave-uniform value in SGPRs at this point of the program (so its load
+// is issued here, together with the others pinned next to it).
+template <typename T>
+__device__ __forceinline__ void pin_sgpr(const T& x) {
+    asm volatile("" ::"s"(x));
+}
+
 // s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
 // The memory clobber keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

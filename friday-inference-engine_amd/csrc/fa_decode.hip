@@ -271,11 +271,22 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     // grid x = (kv head, head block) group, y = split: consecutive workgroup ids walk the
     // groups first, so the dispatch order interleaves groups and, with round-robin
     // placement over the 8 XCDs, the splits of one group share an XCD when there are 8 groups
+    // Kernel arguments are loaded lazily, and loads used only after the early return below
+    // would each cost the prologue a scalar memory round trip: touch every field the
+    // prologue and the first tile need here, so they arrive in one batch.
+    pin_sgpr(p.q); pin_sgpr(p.k); pin_sgpr(p.v); pin_sgpr(p.d_pos); pin_sgpr(p.seq_len); pin_sgpr(p.max_seq);
+    pin_sgpr(p.Hq); pin_sgpr(p.G); pin_sgpr(p.ngb); pin_sgpr(p.kv_dim); pin_sgpr(p.single);
+    pin_sgpr(p.min_chunk); pin_sgpr(p.max_splits); pin_sgpr(p.counters); pin_sgpr(p.merge_slices);
+    pin_sgpr(p.Hkv); pin_sgpr(p.out_q); pin_sgpr(p.scale2); pin_sgpr(p.nsplit_grid);
+    if (PAGED) { pin_sgpr(p.seq_lens); pin_sgpr(p.block_table); pin_sgpr(p.bt_stride); }
+    if (ROPE) { pin_sgpr(p.rope_table); pin_sgpr(p.neox); pin_sgpr(p.k_new); pin_sgpr(p.v_new); }
     const int group = blockIdx.x;
     const int split = blockIdx.y;
     const int kvh = group / p.ngb, gb = group % p.ngb;
     const int b = blockIdx.z;
-    const int S = context_len(p, b, PAGED);
+    // context length: read once (the device position or sequence length), clamped to the cache
+    const int S_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
+    const int S = min(S_raw, p.max_seq);
     const int chunk = p.single ? (S > 0 ? ((S + kSpan - 1) / kSpan) * kSpan : kSpan)
                                : split_chunk(S, p.min_chunk, p.max_splits);
     const int nsp = p.single ? 1 : split_count(S, p.min_chunk, p.max_splits);
@@ -284,7 +295,8 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     // last nslice splits) and, for mergers, the group's counter base, loaded early
     const int nslice = (nsp > 1 && p.counters) ? merge_slices<D>(p, nsp) : 1;
     const int mk = split - (nsp - nslice);
-    unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * kCounterStride;
+    // (grid x = Hkv * ngb groups)
+    unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)b * p.Hkv * p.ngb + group) * kCounterStride;
     unsigned base = 0;
     if (nsp > 1 && p.counters && mk >= 0)
         base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -302,14 +314,6 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     // Loads are unconditional (lanes past the group read the group's first head and are
     // zeroed later), so no branch drains the load counter.
     h8 qf[Gm::KSTEPS];
-    {
-        const uint16_t* qrow = p.q + ((size_t)b * p.Hq + (gvalid ? head : kvh * p.G)) * D;
-#pragma unroll
-        for (int s = 0; s < Gm::KSTEPS; ++s) {
-            const u4 raw = *reinterpret_cast<const u4*>(qrow + s * 32 + kb * 8);
-            qf[s] = *reinterpret_cast<const h8*>(&raw);
-        }
-    }
 
     // Step variant: the RoPE table entries of this lane's q fragment, and the new K/V row
     // chunk (plus its rotation partner chunk) of lane chunk `lane % CPR`, all at position
@@ -328,6 +332,26 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     bool rot_q = false;
     const int nchunk = (lane % Gm::CPR) * CW;  // first element of this lane's row chunk
     if constexpr (ROPE) {
+        // the wave that loads the tile holding position S-1 (in the split holding it)
+        // takes the new row from registers instead of the cache; past max_seq: no append
+        rot_q = S > 0 && S_raw == S;
+        if (rot_q && split == nsp - 1) {
+            const int last_tile = (end - start - 1) / kTile;
+            append_wave = last_tile % kWaves;
+            append_tile = last_tile;
+            append_row = (S - 1) - (start + last_tile * kTile);
+        }
+    }
+    // The inputs other than the cache (q, the RoPE table entries, the new row): issued after
+    // the first K/V tiles, so that those, the longest wait, start first.
+    auto load_inputs = [&]() __attribute__((always_inline)) {
+        const uint16_t* qrow = p.q + ((size_t)b * p.Hq + (gvalid ? head : kvh * p.G)) * D;
+#pragma unroll
+        for (int s = 0; s < Gm::KSTEPS; ++s) {
+            const u4 raw = *reinterpret_cast<const u4*>(qrow + s * 32 + kb * 8);
+            qf[s] = *reinterpret_cast<const h8*>(&raw);
+        }
+        if constexpr (!ROPE) return;
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
         if (p.neox) {
@@ -336,17 +360,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
 #pragma unroll
                 for (int j = 0; j < 8; ++j) qcs[s * 8 + j] = cs[s * 32 + kb * 8 + j];
         }
-        // the wave that loads the tile holding position S-1 (in the split holding it)
-        // takes the new row from registers instead of the cache; past max_seq: no append
-        const int s_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
-        rot_q = S > 0 && s_raw == S;
-        if (rot_q && split == nsp - 1) {
-            const int last_tile = (end - start - 1) / kTile;
-            append_wave = last_tile % kWaves;
-            append_tile = last_tile;
-            append_row = (S - 1) - (start + last_tile * kTile);
-        }
-        // only that wave needs the new row chunk (and its rotation partner) of its lane
+        // only the append wave needs the new row chunk (and its rotation partner) of its lane
         if (wave == append_wave) {
             const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
             const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
@@ -359,7 +373,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
 #pragma unroll
             for (int j = 0; j < CW; ++j) ncs[j] = cs[p.neox ? (nchunk % HD2) + j : (nchunk + j) / 2];
         }
-    }
+    };
 
     // Rotate this lane's q fragment at position S-1 (neox pairs: k-steps s and
     // s + KSTEPS/2; interleaved pairs: neighbouring elements), then zero lanes past the
@@ -595,6 +609,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
 #pragma unroll
             for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * kWaves);
         }
+        load_inputs();
         prepare();
         for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
