@@ -47,7 +47,8 @@ struct Geo {
     static constexpr int WAVE_LDS = 2 * kTile * LROW;  // K and V tile of one wave
     static constexpr int CROW = D + 4;                 // combine row stride in floats (bank spread)
     static constexpr int COMB_LDS = (2 * kWaves * 16 + kWaves * 16 * CROW) * 4;
-    static constexpr int LDS = kWaves * WAVE_LDS + COMB_LDS;  // tiles, then the wave combine
+    static constexpr int QX_OFF = kWaves * WAVE_LDS + COMB_LDS;  // rotated q rows, 16 heads x D fp16
+    static constexpr int LDS = QX_OFF + 16 * D * 2;              // tiles, the wave combine, the q rows
 };
 
 __device__ __forceinline__ int context_len(const DecodeParams& p, int b, bool paged) {
@@ -320,10 +321,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     // S-1. They are issued before the first K/V tile and used after it is in flight. A
     // chunk is the 16 bytes one lane moves per cache row: 8 fp16 values, or 16 int8 ones.
     constexpr int HD2 = D / 2;
-    constexpr int QCS = ROPE ? (Gm::KSTEPS / 2) * 8 : 1;  // table entries of the q fragment (neox)
+    constexpr int PPT = ROPE ? D / 32 : 1;  // q rotation pairs per thread (16 head columns x D/2 pairs)
     constexpr int CW = Q8 ? 16 : 8;                       // values of one row chunk
     constexpr int NH = ROPE ? CW / 8 : 1;                 // fp16 vectors of one row chunk
-    float2 qcs[QCS];
+    _Float16 rq0[PPT], rq1[PPT];
+    float2 rcs[PPT];
     h8 nk[NH], nkp[NH], nv[NH];
     float2 ncs[ROPE ? CW : 1];
     int append_wave = -1, append_tile = -1, append_row = -1;
@@ -354,11 +356,16 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         if constexpr (!ROPE) return;
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
-        if (p.neox) {
+        if (rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / 16
+            const int hg = gb * 16 + (tid >> 4), i0 = (tid & 15) * PPT;
+            const uint16_t* qr = p.q + ((size_t)b * p.Hq + kvh * p.G + (hg < p.G ? hg : 0)) * D;
 #pragma unroll
-            for (int s = 0; s < Gm::KSTEPS / 2; ++s)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qcs[s * 8 + j] = cs[s * 32 + kb * 8 + j];
+            for (int e = 0; e < PPT; ++e) {
+                const int i = i0 + e;  // pair (i, i + D/2) (neox) or (2i, 2i + 1)
+                rq0[e] = *reinterpret_cast<const _Float16*>(qr + (p.neox ? i : 2 * i));
+                rq1[e] = *reinterpret_cast<const _Float16*>(qr + (p.neox ? i + HD2 : 2 * i + 1));
+                rcs[e] = cs[i];
+            }
         }
         // only the append wave needs the new row chunk (and its rotation partner) of its lane
         if (wave == append_wave) {
@@ -386,31 +393,24 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     float ksc = 0.0f, vsc = 0.0f;
     auto prepare = [&]() __attribute__((always_inline)) {
         if constexpr (ROPE) {
-            if (!rot_q) {
-                // position outside the cache: q keeps its values, no row is appended
-            } else if (p.neox) {
+            if (rot_q) {
+                // The rotation of the group's q rows is spread over the 256 threads (thread t:
+                // rotation pairs i0 .. i0 + PPT - 1 of head column t / 16, from the values
+                // load_inputs fetched), and every lane reads its rotated fragment back from LDS.
+                _Float16* qx = reinterpret_cast<_Float16*>(smem + Gm::QX_OFF);  // [16 heads][D]
+                const int hc = tid >> 4, i0 = (tid & 15) * PPT;
 #pragma unroll
-                for (int s = 0; s < Gm::KSTEPS / 2; ++s)
+                for (int e = 0; e < PPT; ++e) {
+                    if (p.neox)
+                        rope_rotate((float)rq0[e], (float)rq1[e], rcs[e].x, rcs[e].y, qx[hc * D + i0 + e],
+                                    qx[hc * D + HD2 + i0 + e]);
+                    else
+                        rope_rotate((float)rq0[e], (float)rq1[e], rcs[e].x, rcs[e].y, qx[hc * D + 2 * (i0 + e)],
+                                    qx[hc * D + 2 * (i0 + e) + 1]);
+                }
+                __syncthreads();
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float2 c = qcs[s * 8 + j];
-                        _Float16 r0, r1;
-                        rope_rotate((float)qf[s][j], (float)qf[s + Gm::KSTEPS / 2][j], c.x, c.y, r0, r1);
-                        qf[s][j] = r0;
-                        qf[s + Gm::KSTEPS / 2][j] = r1;
-                    }
-            } else {
-                const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)(S > 0 ? S - 1 : 0) * HD2;
-#pragma unroll
-                for (int s = 0; s < Gm::KSTEPS; ++s)
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        const float2 c = cs[(s * 32 + kb * 8 + j) / 2];
-                        _Float16 r0, r1;
-                        rope_rotate((float)qf[s][j], (float)qf[s][j + 1], c.x, c.y, r0, r1);
-                        qf[s][j] = r0;
-                        qf[s][j + 1] = r1;
-                    }
+                for (int s = 0; s < Gm::KSTEPS; ++s) qf[s] = *reinterpret_cast<const h8*>(qx + col * D + s * 32 + kb * 8);
             }
             if (wave == append_wave) {
                 h8 r[NH];
