@@ -120,6 +120,28 @@ __device__ __forceinline__ float2 ld_coherent2(__amdgpu_buffer_rsrc_t r, uint32_
     return *reinterpret_cast<const float2*>(&x);
 }
 
+// Buffer descriptor from wave-uniform values, built from SGPRs (readfirstlane): without it
+// the compiler may treat the descriptor as divergent and wrap every load in a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const void* ptr = reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)__builtin_amdgcn_readfirstlane(bytes),
+                                             0x00020000);
+}
+
+// Nontemporal buffer loads (cache policy nt): 16 bytes, and one fp16 value as a float.
+// Offsets at or past the descriptor's byte count read as zero.
+constexpr int kCpolNt = 2;
+__device__ __forceinline__ u4 ld_buf_nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const i4v x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCpolNt);
+    return *reinterpret_cast<const u4*>(&x);
+}
+__device__ __forceinline__ float ld_buf_f16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const short x = __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, kCpolNt);
+    return (float)__builtin_bit_cast(_Float16, x);
+}
+
 __device__ __forceinline__ void st_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const i4v*>(&v), r, (int)byte_off, 0, kCpolSc1);
 }

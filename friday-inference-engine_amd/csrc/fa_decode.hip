@@ -32,7 +32,8 @@ constexpr int kStages = 1;    // register stages (tiles in flight) per wave
 // int8 rows are half as wide: twice the tiles in flight keep the same bytes in flight
 constexpr int kStagesQ8 = 2;
 constexpr int kShortStages = 4;
-constexpr int kMergeSlices = 8;  // column slices of the distributed fused merge            // stages when a wave has at most this many tiles
+constexpr int kMergeSlices = 8;  // column slices of the distributed fused merge
+constexpr float kLazy2 = 8.0f;   // lazy softmax reference: rescale when a max rises by > 2^8            // stages when a wave has at most this many tiles
 
 template <int D, bool Q8>
 struct Geo {
@@ -491,54 +492,99 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         float ks[Gm::NLD], vs[Gm::NLD];
     };
 
-    // A tile past the end (the refill after a wave's last tile) reads this workgroup's q row
-    // instead: valid memory that is already cached, so its loads are cheap to wait for.
+    // Contiguous caches: each tile is read through buffer descriptors that cover exactly its
+    // rows inside [start, end), so rows past the end, and whole tiles past the last one (the
+    // refill after a wave's last tile), read as zeros without touching memory; the lane's
+    // byte offsets are the same for every tile. Paged pools go through the block table, rows
+    // clamped to the split and a tile past the end reading this workgroup's q row instead.
     const char* qrow_bytes = reinterpret_cast<const char*>(p.q + (size_t)b * p.Hq * D + (size_t)kvh * p.G * D);
+    const uint32_t lane_off = (uint32_t)(lrow * rowb + lchunk * 16);
+    const uint32_t srow = (uint32_t)(p.kv_dim / 32) * 2;  // bytes of one position's int8 scales
+    const uint32_t lane_soff = (uint32_t)lrow * srow + (uint32_t)(lchunk * 16 / 32) * 2;
     auto load_tile = [&](Stage& st, int t) {
         const int base = start + t * kTile;
-        const bool past = t >= ntiles;  // uniform
-        const char* kb = past ? qrow_bytes : kbase;
-        const char* vb = past ? qrow_bytes : vbase;
+        if constexpr (!PAGED) {
+            const uint32_t nrows = (uint32_t)min(max(end - base, 0), kTile);
+            const __amdgpu_buffer_rsrc_t rk = uniform_rsrc(kbase + (size_t)base * rowb, nrows * (uint32_t)rowb);
+            const __amdgpu_buffer_rsrc_t rv = uniform_rsrc(vbase + (size_t)base * rowb, nrows * (uint32_t)rowb);
 #pragma unroll
-        for (int r = 0; r < Gm::NLD; ++r) {
-            const int pos = base + r * Gm::RPI + lrow;
-            const size_t ri = past ? 0 : row_index<PAGED>(p, b, max(min(pos, end - 1), start));
-            st.k[r] = ld_nt(reinterpret_cast<const u4*>(kb + ri * rowb) + lchunk);
-            st.v[r] = ld_nt(reinterpret_cast<const u4*>(vb + ri * rowb) + lchunk);
-            if (Q8) {
-                const size_t si = (ri * p.kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
-                st.ks[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
-                st.vs[r] = (float)*reinterpret_cast<const _Float16*>(p.v_scale + si);
+            for (int r = 0; r < Gm::NLD; ++r) {
+                st.k[r] = ld_buf_nt(rk, lane_off + (uint32_t)(r * Gm::RPI) * (uint32_t)rowb);
+                st.v[r] = ld_buf_nt(rv, lane_off + (uint32_t)(r * Gm::RPI) * (uint32_t)rowb);
+            }
+            if constexpr (Q8) {
+                const size_t sb = (size_t)base * (p.kv_dim / 32) + (size_t)kvh * (D / 32);
+                const __amdgpu_buffer_rsrc_t rks = uniform_rsrc(p.k_scale + sb, nrows * srow);
+                const __amdgpu_buffer_rsrc_t rvs = uniform_rsrc(p.v_scale + sb, nrows * srow);
+#pragma unroll
+                for (int r = 0; r < Gm::NLD; ++r) {
+                    st.ks[r] = ld_buf_f16(rks, lane_soff + (uint32_t)(r * Gm::RPI) * srow);
+                    st.vs[r] = ld_buf_f16(rvs, lane_soff + (uint32_t)(r * Gm::RPI) * srow);
+                }
+            }
+        } else {
+            const bool past = t >= ntiles;  // uniform
+            const char* kb = past ? qrow_bytes : kbase;
+            const char* vb = past ? qrow_bytes : vbase;
+#pragma unroll
+            for (int r = 0; r < Gm::NLD; ++r) {
+                const int pos = base + r * Gm::RPI + lrow;
+                const size_t ri = past ? 0 : row_index<PAGED>(p, b, max(min(pos, end - 1), start));
+                st.k[r] = ld_nt(reinterpret_cast<const u4*>(kb + ri * rowb) + lchunk);
+                st.v[r] = ld_nt(reinterpret_cast<const u4*>(vb + ri * rowb) + lchunk);
+                if (Q8) {
+                    const size_t si = (ri * p.kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
+                    st.ks[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
+                    st.vs[r] = (float)*reinterpret_cast<const _Float16*>(p.v_scale + si);
+                }
             }
         }
     };
 
     auto consume = [&](Stage& st, int t, int t_next) {
         const int tbase = start + t * kTile;
-        // registers -> wave-private LDS tile (rows past the end as zeros)
+        if constexpr (Q8) {
+            // int8 rows: take the raw codes and scales out of the stage, refill it at once, and
+            // dequantise into the wave's LDS tile while the refill is in flight
+            u4 ck[Gm::NLD], cv[Gm::NLD];
+            float sk[Gm::NLD], sv[Gm::NLD];
 #pragma unroll
-        for (int r = 0; r < Gm::NLD; ++r) {
-            const int row = r * Gm::RPI + lrow;
-            const bool live = tbase + row < end;
-            if (Q8) {
-                u4 lo, hi;
-                u4 ck = st.k[r], cv = st.v[r];
-                float sk = live ? st.ks[r] : 0.0f, sv = live ? st.vs[r] : 0.0f;
+            for (int r = 0; r < Gm::NLD; ++r) {
+                const int row = r * Gm::RPI + lrow;
+                const bool live = tbase + row < end;
+                ck[r] = st.k[r];
+                cv[r] = st.v[r];
+                sk[r] = (!PAGED || live) ? st.ks[r] : 0.0f;  // contiguous: zeros past the end already
+                sv[r] = (!PAGED || live) ? st.vs[r] : 0.0f;
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
-                    ck = kq;  // the new row, as quantized and written to the cache by this wave
-                    cv = vq;
-                    sk = ksc;
-                    sv = vsc;
+                    ck[r] = kq;  // the new row, as quantized and written to the cache by this wave
+                    cv[r] = vq;
+                    sk[r] = ksc;
+                    sv[r] = vsc;
                 }
-                dequant16(ck, sk, lo, hi);
+            }
+            load_tile(st, t_next);
+#pragma unroll
+            for (int r = 0; r < Gm::NLD; ++r) {
+                const int row = r * Gm::RPI + lrow;
+                u4 lo, hi;
+                dequant16(ck[r], sk[r], lo, hi);
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32) = lo;
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32 + 16) = hi;
-                dequant16(cv, sv, lo, hi);
+                dequant16(cv[r], sv[r], lo, hi);
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32) = lo;
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32 + 16) = hi;
-            } else {
+            }
+            // LDS operations of one wave complete in order: the reads below see these writes.
+            __builtin_amdgcn_wave_barrier();
+        } else {
+            // registers -> wave-private LDS tile (rows past the end as zeros)
+#pragma unroll
+            for (int r = 0; r < Gm::NLD; ++r) {
+                const int row = r * Gm::RPI + lrow;
+                const bool live = tbase + row < end;
                 const u4 z = u4{0, 0, 0, 0};
-                u4 kx = live ? st.k[r] : z, vx = live ? st.v[r] : z;
+                u4 kx = (!PAGED || live) ? st.k[r] : z, vx = (!PAGED || live) ? st.v[r] : z;  // contiguous: zeros already
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
                     kx = rk;  // the new row, as written to the cache by this wave
                     vx = *reinterpret_cast<const u4*>(&nv[0]);
@@ -546,12 +592,12 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
                 *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = kx;
                 *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = vx;
             }
+            // LDS operations of one wave complete in order: the reads below see these writes.
+            __builtin_amdgcn_wave_barrier();
+            // Refill this stage while computing. Unconditional, so no branch hides loads from
+            // the wait counter: a tile past the end reads this wave's q row instead.
+            load_tile(st, t_next);
         }
-        // LDS operations of one wave complete in order: the reads below see these writes.
-        __builtin_amdgcn_wave_barrier();
-        // Refill this stage while computing. Unconditional, so no branch hides loads from the
-        // wait counter: a tile past the end reads this wave's q row instead (L1-resident).
-        load_tile(st, t_next);
         if (t >= ntiles) return;  // uniform: this stage held no tile
 
         // S^T[16 positions x 16 heads] = K Q^T
@@ -573,26 +619,34 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
             mx = fmaxf(mx, sc[i]);
         }
         mx = col_max4(mx);  // over the 4 lane blocks: the 16 positions of the tile
-        const float m_new = fmaxf(m_run, mx);
-        const float da = m_run - m_new;
-        const float alpha = da < kCut2 ? 0.0f : exp2_fast(da);
+        // Lazy reference max: the accumulators move to a new reference (and are rescaled) only
+        // when some head's tile max exceeds its reference by more than 2^8 (a wave-uniform
+        // branch, rarely taken after the first tile); weights stay <= 256 in between.
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazy2) != 0) {
+            const float m_new = fmaxf(m_run, mx);
+            const float da = m_run - m_new;
+            const float alpha = da < kCut2 ? 0.0f : exp2_fast(da);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < Gm::DTILES; ++dt) o[dt] *= alpha;
+            m_run = m_new;
+        }
         h4 pf;
         float psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float df = sc[i] - m_new;  // -inf for masked rows
+            const float df = sc[i] - m_run;  // -inf for masked rows
             const _Float16 eh = (_Float16)(df < kCut2 ? 0.0f : exp2_fast(df));
             pf[i] = eh;
             psum += (float)eh;
         }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
+        l_run += psum;
 
         // O^T += V^T P^T over the 16 positions (k = kb*4 + i); V^T by one transposing LDS read
 #pragma unroll
         for (int dt = 0; dt < Gm::DTILES; ++dt) {
             const h4 va = lds_read_tr16(vl + (kb * 4 + (col >> 2)) * Gm::LROW + (dt * 16 + 4 * (col & 3)) * 2);
-            o[dt] = mfma16x16x16(va, pf, o[dt] * alpha);
+            o[dt] = mfma16x16x16(va, pf, o[dt]);
         }
         __builtin_amdgcn_wave_barrier();
     };
