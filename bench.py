@@ -40,10 +40,12 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 MALL_BYTES = 256 << 20         # Infinity Cache: a "cold" working set must exceed it
 
-# HBM traffic of one step-kernel launch at the headline shape, from rocprofv3 --pmc
-# FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by the copy-kernel calibration
-# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): 135.16 MB fetched + 0.76 MB written per launch.
+# HBM traffic of one step-kernel launch at the headline shape: a constant taken from the
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs recorded in the profile below (KiB per
+# dispatch, scaled by the copy-kernel calibration FETCH_SIZE x 2.0, WRITE_SIZE x 1.0);
+# it is not measured in this run.
 HEADLINE_TRAFFIC_BYTES = 135924531
+TRAFFIC_SOURCE = "constant from profiles/decode_step_cfg3_pmc.txt (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)"
 
 
 def log(msg):
@@ -67,8 +69,10 @@ class Ctx:
     def fill(self, buf, n_half, seed, scale=1.0):
         self.bk.fabk_fill_normal_f16(buf.ptr, n_half, seed, scale, self.stream.s)
 
-    def timed(self, fn, steps, warmup):
-        """Capture fn's launches into a graph; replay warmup + steps times; ms per replay."""
+    def timed(self, fn, steps, warmup, stats=0):
+        """Capture fn's launches into a graph; replay warmup + steps times; ms per replay.
+        stats > 0: afterwards time that many further replays one by one (HIP events between
+        consecutive replays) and return (ms per replay, {median, p10, p90} in ms)."""
         fa = self.fa
         graph = fa.Graph(self.stream, fn)
         for _ in range(warmup):
@@ -80,7 +84,20 @@ class Ctx:
             graph.launch()
         t1.record(self.stream.s)
         self.stream.synchronize()
-        return t0.elapsed_ms(t1) / steps
+        ms = t0.elapsed_ms(t1) / steps if steps else 0.0
+        if not stats:
+            return ms
+        import numpy as np
+
+        ev = [fa.Event() for _ in range(stats + 1)]
+        ev[0].record(self.stream.s)
+        for i in range(stats):
+            graph.launch()
+            ev[i + 1].record(self.stream.s)
+        self.stream.synchronize()
+        d = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(stats)])
+        return ms, {"replays": stats, "median_ms": round(float(np.median(d)), 4),
+                    "p10_ms": round(float(np.percentile(d, 10)), 4), "p90_ms": round(float(np.percentile(d, 90)), 4)}
 
 
 class DecodeLayers:
@@ -131,11 +148,14 @@ class DecodeLayers:
             fa.launchDecodeAttentionFused(q, kc, vc, out, 0, self.pos, self.S, self.Hq, self.Hkv, self.d, self.ws,
                                           cx.stream.s)
 
-    def measure(self, steps, warmup, fn="step"):
-        """ms per decode step; with several sets each replay walks all of them (cold caches)."""
+    def measure(self, steps, warmup, fn="step", stats=0):
+        """ms per decode step; with several sets each replay walks all of them (cold caches).
+        stats > 0: also the per-replay distribution (see Ctx.timed)."""
         f = getattr(self, fn)
-        ms = self.cx.timed(lambda: [f(s) for s in range(self.sets)], steps, warmup)
-        return ms / self.sets
+        r = self.cx.timed(lambda: [f(s) for s in range(self.sets)], steps, warmup, stats)
+        if stats:
+            return r[0] / self.sets, r[1]
+        return r / self.sets
 
     def check_layer0(self):
         import numpy as np
@@ -159,7 +179,19 @@ class DecodeLayers:
             b.free()
 
 
-def cpu_baseline(S, Hq, Hkv, d, budget_s):
+# The GPU box gives one GPU's job a share of 16 logical CPUs, whatever os.cpu_count() reports.
+CPU_SHARE = 16
+
+
+def cpu_thread_counts(Hq):
+    """The two thread counts the CPU baseline is timed at: min(logical CPUs, Hq) (the
+    reference parallelises decode attention over query heads, cpu_ops.cpp:50) and the
+    reference's default pool size, 2/3 of the logical CPUs (cpu_backend.cpp:45-50)."""
+    ncpu = min(os.cpu_count() or 1, CPU_SHARE)
+    return max(1, min(ncpu, Hq)), (ncpu * 2 // 3 if ncpu >= 3 else 1)
+
+
+def cpu_baseline(S, Hq, Hkv, d, budget_s, threads=None):
     """Reference CPU decode attention (cpu_ops.cpp:45-83) on a bounded sample."""
     import numpy as np
 
@@ -167,7 +199,8 @@ def cpu_baseline(S, Hq, Hkv, d, budget_s):
     import py_oracle
 
     ncpu = os.cpu_count() or 1
-    threads = max(1, min(16, ncpu, Hq))  # parallel over query heads; the GPU box's CPU share is 16
+    if threads is None:
+        threads = cpu_thread_counts(Hq)[0]
     rng = np.random.default_rng(0)
     kv_dim = Hkv * d
     kc = rng.standard_normal((S, kv_dim), dtype=np.float32).astype(np.float16).astype(np.float32)
@@ -204,6 +237,7 @@ def headline(cx, args):
     log(f"[bench] config 3: S={S} layers={L} {Hq}q/{Hkv}kv d{d}, {2 * L * S * Hkv * d * 2 / 2**30:.2f} GiB KV")
     dl = DecodeLayers(cx, S, L, Hq, Hkv, d)
     ms_step = dl.measure(args.steps, args.warmup, "step")
+    _, step_stats = dl.measure(0, 0, "step", stats=args.stat_replays)
     ms_dec = dl.measure(args.steps, args.warmup, "decode_only")
     check = None if args.no_check else dl.check_layer0()
     dl.free()
@@ -212,10 +246,12 @@ def headline(cx, args):
     gbs = kv_bytes / (us_layer * 1e-6) / 1e9
     log(f"[bench] {ms_step:.3f} ms/step, {us_layer:.2f} us/layer-step ({gbs:.0f} GB/s), "
         f"decode-only launch {ms_dec * 1e3 / L:.2f} us")
-    cpu = None
+    cpu = cpu_ref_default = None
     if not args.no_cpu:
-        log("[bench] timing the reference CPU attention ...")
-        cpu = cpu_baseline(S, Hq, Hkv, d, args.cpu_seconds)
+        t_heads, t_default = cpu_thread_counts(Hq)
+        log(f"[bench] timing the reference CPU attention ({t_heads} and {t_default} threads) ...")
+        cpu = cpu_baseline(S, Hq, Hkv, d, args.cpu_seconds / 2, threads=t_heads)
+        cpu_ref_default = cpu_baseline(S, Hq, Hkv, d, args.cpu_seconds / 2, threads=t_default)
     return {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -240,8 +276,13 @@ def headline(cx, args):
         "roofline": {"bound": "hbm", "kernel": "fa_decode_kernel (step variant: friday_attn_decode_step)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": HEADLINE_TRAFFIC_BYTES,
+                     "traffic_source": TRAFFIC_SOURCE,
                      "algorithmic_bytes_per_launch": kv_bytes, "launches_per_step": L},
+        "step_stats": {**step_stats, "us_per_layer_median": round(step_stats["median_ms"] * 1e3 / L, 3),
+                       "us_per_layer_p10": round(step_stats["p10_ms"] * 1e3 / L, 3),
+                       "us_per_layer_p90": round(step_stats["p90_ms"] * 1e3 / L, 3)},
         "cpu_baseline": cpu,
+        "cpu_baseline_reference_default_threads": cpu_ref_default,
         "check": check,
     }
 
@@ -259,6 +300,41 @@ def decode_config(cx, name, S, L, Hq, Hkv, d, steps, warmup, cold):
     return {"config": name, "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}", "cache": "cold" if cold else "warm",
             "working_set_MiB": round(sets * L * kv_bytes / 2**20, 1), "us_per_layer_step": round(us, 3),
             "kv_GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(1e3 / ms, 1)}
+
+
+def append_config(cx, T, steps, warmup):
+    """RoPE + KV append (friday_attn_rope_store_kv, ropeStoreKvKernel semantics) at the
+    headline shapes (40q/8kv, d128): T = 1 (a decode token) or T = 512 (a prefill chunk),
+    one launch per layer over 64 layers' inputs and caches. Algorithmic bytes per token:
+    read q, k, v and the RoPE table row ((Hq + 2 Hkv) d 2 + d/2 8), written q and k in
+    place and the k and v cache rows ((Hq + 3 Hkv) d 2)."""
+    import numpy as np
+
+    fa = cx.fa
+    Hq, Hkv, d, L, max_ctx = 40, 8, 128, 64, 8192
+    kv_dim = Hkv * d
+    q, k, v = (fa.DeviceBuffer(L * T * n * 2) for n in (Hq * d, kv_dim, kv_dim))
+    for bb, n in ((q, Hq * d), (k, kv_dim), (v, kv_dim)):
+        cx.fill(bb, L * T * n, 30 + n)
+    kc, vc = fa.DeviceBuffer(L * max_ctx * kv_dim * 2), fa.DeviceBuffer(L * max_ctx * kv_dim * 2)
+    table = fa.DeviceBuffer(fa.rope_table_bytes(max_ctx, d))
+    fa.rope_table_upload(table, max_ctx, d, 1e6)
+    pos = fa.DeviceBuffer.from_array(np.array([max_ctx - T - 1], np.int32))
+
+    def run():
+        for l in range(L):
+            fa.ropeStoreKv(q.ptr + l * T * Hq * d * 2, k.ptr + l * T * kv_dim * 2, v.ptr + l * T * kv_dim * 2,
+                           kc.ptr + l * max_ctx * kv_dim * 2, vc.ptr + l * max_ctx * kv_dim * 2, pos, 0, T, d, Hq, Hkv,
+                           max_ctx, table, 1, cx.stream.s)
+
+    ms = cx.timed(run, steps, warmup) / L
+    for bb in (q, k, v, kc, vc, table, pos):
+        bb.free()
+    per_token = (Hq + 2 * Hkv) * d * 2 + d // 2 * 8 + (Hq + 3 * Hkv) * d * 2
+    gbs = T * per_token / (ms * 1e-3) / 1e9
+    return {"config": "RoPE + KV append (ropeStoreKvKernel)", "T": T, "heads": f"{Hq}q/{Hkv}kv d{d}",
+            "us_per_layer": round(ms * 1e3, 3), "bytes_per_layer": T * per_token, "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def prefill_config(cx, p0, steps, warmup, q8=False):
@@ -513,13 +589,15 @@ def main():
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--stat-replays", type=int, default=100,
+                    help="further replays timed one by one for the median / p10 / p90 of a step")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
                     help="only copy 1 GiB three times with the bench-kit streaming copy (one 16-byte load and "
                          "store per element): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run give the "
                          "counters' reading for a known 1 GiB read + 1 GiB write")
-    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm", "layer"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm", "layer", "append"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other benchmark configs of BASELINE.json")
     args = ap.parse_args()
 
@@ -553,6 +631,8 @@ def main():
         for p0 in (0, 7680):
             lines.append(prefill_config(cx, p0, args.steps, args.warmup, q8=True))
         lines.append(paged_config(cx, args.steps, args.warmup))
+        for T in (1, 512):
+            lines.append(append_config(cx, T, args.steps, args.warmup))
         lines.append(q8_config(cx, 32768, 64, args.steps, args.warmup))
         for case in GEMM_CASES:
             lines.append(gemm_config(cx, *case, args.steps, args.warmup))
@@ -564,6 +644,9 @@ def main():
             print(json.dumps(rec), flush=True)
     if args.config == "q8":
         print(json.dumps(q8_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
+    if args.config == "append":
+        for T in (1, 512):
+            print(json.dumps(append_config(cx, T, args.steps, args.warmup)), flush=True)
     if args.config == "paged":
         print(json.dumps(paged_config(cx, args.steps, args.warmup)), flush=True)
     if args.config == "prefill":

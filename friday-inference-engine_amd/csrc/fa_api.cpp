@@ -44,6 +44,12 @@ int launch_status(int rc, const char* what) {
 
 bool head_dim_ok(int d) { return d == 64 || d == 128; }
 
+// The append moves 16-byte chunks: every tensor it touches must be 16-byte aligned (null is fine).
+bool aligned16(const void* a, const void* b, const void* c, const void* d, const void* e) {
+    return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c) |
+             reinterpret_cast<uintptr_t>(d) | reinterpret_cast<uintptr_t>(e)) & 15) == 0;
+}
+
 // Shape rules of the reference launchers (attention_kernels.cu:416-419, 450-454).
 int check_heads(const char* what, int Hq, int Hkv, int d) {
     if (!head_dim_ok(d)) return fail(FA_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128 (got %d)", what, d);
@@ -163,6 +169,7 @@ int friday_attn_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint1
         return fail(FA_ERR_INVALID, "%s: k_layer, v_layer and v must be given together", w);
     if (!d_pos && (pos < 0 || pos + T > max_ctx))
         return fail(FA_ERR_INVALID, "%s: positions [%d, %d) exceed max_ctx %d", w, pos, pos + T, max_ctx);
+    if (!aligned16(q, k, v, k_layer, v_layer)) return fail(FA_ERR_INVALID, "%s: q, k, v and caches must be 16-byte aligned", w);
     fa::RopeParams p{};
     p.q = q; p.k = k; p.v = v; p.k_dst = k_layer; p.v_dst = v_layer; p.table = rope_table;
     p.d_pos = d_pos; p.pos = pos; p.T = T; p.D = head_dim; p.Hq = num_q_heads; p.Hkv = num_kv_heads;
@@ -459,6 +466,7 @@ int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v,
     if (batch <= 0 || max_ctx <= 0 || !q || !k || !v || !k_pool || !v_pool || !block_table || !seq_lens ||
         !rope_table || block_table_stride <= 0 || (long long)block_table_stride * FA_PAGE_TOKENS < max_ctx)
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
+    if (!aligned16(q, k, v, k_pool, v_pool)) return fail(FA_ERR_INVALID, "%s: q, k, v and pools must be 16-byte aligned", w);
     fa::RopeParams p{};
     p.q = q; p.k = k; p.v = v; p.k_dst = k_pool; p.v_dst = v_pool; p.table = rope_table;
     p.block_table = block_table; p.bt_stride = block_table_stride; p.seq_lens = seq_lens;

@@ -13,28 +13,53 @@
 namespace fa {
 namespace {
 
-// One thread per (token, head, rotation pair). Heads [0, Hq) are query heads,
-// [Hq, Hq + Hkv) key heads (their thread also moves the matching v pair).
+// One thread per (token, head, 16-byte chunk): 128-bit loads and stores of 8 fp16 values.
+// Heads [0, Hq) are query heads, [Hq, Hq + Hkv) key heads (their thread also moves the
+// matching v chunks). NeoX pairs (i, i + D/2): a thread takes the chunk of elements
+// [8c, 8c + 8) and its partner chunk [D/2 + 8c, ...), 8 pairs; interleaved pairs: the
+// chunk [8c, 8c + 8), 4 pairs (2i, 2i + 1).
 template <bool PAGED>
 __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
     const int t = blockIdx.y;
     const int hd2 = p.D >> 1;
+    const int cpp = p.neox ? hd2 / 8 : p.D / 8;  // threads per head
     const int idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (p.Hq + p.Hkv) * hd2) return;
-    const int h = idx / hd2, i = idx - h * hd2;
+    if (idx >= (p.Hq + p.Hkv) * cpp) return;
+    const int h = idx / cpp, c = idx - h * cpp;
     const int pos = PAGED ? p.seq_lens[t] - 1 : (p.d_pos ? *p.d_pos : p.pos) + t;
     if (pos < 0 || pos >= p.max_ctx) return;
-    const float2 cs = reinterpret_cast<const float2*>(p.table)[(size_t)pos * hd2 + i];
-    const int o0 = p.neox ? i : 2 * i;
-    const int o1 = p.neox ? i + hd2 : 2 * i + 1;
+    const float2* cs = reinterpret_cast<const float2*>(p.table) + (size_t)pos * hd2;
     const int kv_dim = p.Hkv * p.D;
     const bool is_k = h >= p.Hq;
     _Float16* x = is_k ? reinterpret_cast<_Float16*>(p.k) + (size_t)t * kv_dim + (h - p.Hq) * p.D
                        : reinterpret_cast<_Float16*>(p.q) + (size_t)t * p.Hq * p.D + h * p.D;
-    _Float16 r0, r1;
-    rope_rotate((float)x[o0], (float)x[o1], cs.x, cs.y, r0, r1);
-    x[o0] = r0;
-    x[o1] = r1;
+    // element offsets of the chunk (and, NeoX, its partner chunk)
+    const int e0 = 8 * c, e1 = p.neox ? hd2 + 8 * c : 8 * c;
+    h8 a = *reinterpret_cast<const h8*>(x + e0);
+    h8 bv = *reinterpret_cast<const h8*>(x + e1);
+    h8 ra, rb;
+    if (p.neox) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float2 r = cs[e0 + j];
+            _Float16 r0, r1;
+            rope_rotate((float)a[j], (float)bv[j], r.x, r.y, r0, r1);
+            ra[j] = r0;
+            rb[j] = r1;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const float2 r = cs[(e0 + j) >> 1];
+            _Float16 r0, r1;
+            rope_rotate((float)a[j], (float)a[j + 1], r.x, r.y, r0, r1);
+            ra[j] = r0;
+            ra[j + 1] = r1;
+        }
+        rb = ra;
+    }
+    *reinterpret_cast<h8*>(x + e0) = ra;
+    if (p.neox) *reinterpret_cast<h8*>(x + e1) = rb;
     if (is_k && p.k_dst) {
         size_t row;
         if (PAGED) {
@@ -47,10 +72,12 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
         _Float16* kd = reinterpret_cast<_Float16*>(p.k_dst) + off;
         _Float16* vd = reinterpret_cast<_Float16*>(p.v_dst) + off;
         const _Float16* vs = reinterpret_cast<const _Float16*>(p.v) + (size_t)t * kv_dim + (h - p.Hq) * p.D;
-        kd[o0] = r0;
-        kd[o1] = r1;
-        vd[o0] = vs[o0];
-        vd[o1] = vs[o1];
+        *reinterpret_cast<h8*>(kd + e0) = ra;
+        *reinterpret_cast<h8*>(vd + e0) = *reinterpret_cast<const h8*>(vs + e0);
+        if (p.neox) {
+            *reinterpret_cast<h8*>(kd + e1) = rb;
+            *reinterpret_cast<h8*>(vd + e1) = *reinterpret_cast<const h8*>(vs + e1);
+        }
     }
 }
 
@@ -88,8 +115,8 @@ __global__ __launch_bounds__(256) void fa_store_kv_q8_kernel(Q8StoreParams p) {
 }  // namespace
 
 int launch_rope_store(const RopeParams& p, bool paged, hipStream_t stream) {
-    const int pairs = (p.Hq + p.Hkv) * (p.D / 2);
-    const dim3 grid((pairs + 255) / 256, p.T);
+    const int threads = (p.Hq + p.Hkv) * (p.neox ? p.D / 16 : p.D / 8);
+    const dim3 grid((threads + 255) / 256, p.T);
     if (paged)
         hipLaunchKernelGGL(fa_rope_store_kernel<true>, grid, dim3(256), 0, stream, p);
     else

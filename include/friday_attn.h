@@ -67,7 +67,9 @@ int friday_attn_rope_table_upload(float* d_table, int max_ctx, int head_dim, flo
  * P + t with P = *d_pos when d_pos != NULL, else P = pos. q [T][Hq*d] and
  * k [T][Hkv*d] are rotated in place (fp32 math, NaN -> 0, clamp, RNE fp16);
  * rotated k and raw v are written to row P + t of k_layer / v_layer.
- * Positions >= max_ctx are skipped (the reference would write out of bounds). */
+ * Positions >= max_ctx are skipped (the reference would write out of bounds). The kernel
+ * moves 16-byte chunks: q, k, v and the caches must be 16-byte aligned (FA_ERR_INVALID
+ * otherwise; device allocations and row offsets of the reference's layout always are). */
 int friday_attn_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_layer, uint16_t* v_layer,
                               const int* d_pos, int pos, int T, int head_dim, int num_q_heads, int num_kv_heads,
                               int max_ctx, const float* rope_table, int neox, void* stream);
@@ -190,8 +192,8 @@ int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const 
  * friday_attn_decode_attention_split over the same logical rows. The decode uses the
  * fused merge: its workspace must be initialised once with friday_attn_decode_workspace_init. */
 size_t friday_attn_paged_workspace_bytes(int batch, int num_heads, int max_seq_len);
-/* Append one token per sequence at position seq_lens[b] - 1 (RoPE as above).
- * q [B][Hq*d], k/v [B][Hkv*d] rotated in place. */
+/* Append one token per sequence at position seq_lens[b] - 1 (RoPE as above, same
+ * 16-byte alignment rule). q [B][Hq*d], k/v [B][Hkv*d] rotated in place. */
 int friday_attn_paged_rope_store_kv(uint16_t* q, uint16_t* k, const uint16_t* v, uint16_t* k_pool, uint16_t* v_pool,
                                     const int32_t* block_table, int block_table_stride, const int32_t* seq_lens,
                                     int batch, int head_dim, int num_q_heads, int num_kv_heads, int max_ctx,

@@ -89,6 +89,10 @@ def test_append_validation(fa):
     # no rope table
     assert L.friday_attn_rope_store_kv(FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, 1, 128, 40, 8, 10, None, 1,
                                        None) == fa.FA_ERR_INVALID
+    # the append moves 16-byte chunks: misaligned tensors are rejected
+    assert L.friday_attn_rope_store_kv(FAKE + 2, FAKE, FAKE, FAKE, FAKE, None, 0, 1, 128, 40, 8, 10, FAKE, 1,
+                                       None) == fa.FA_ERR_INVALID
+    assert "aligned" in err(fa)
     # int8: kv_dim must be a multiple of 32
     assert L.friday_attn_store_kv_q8(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 0, 1, 100, 10,
                                      None) == fa.FA_ERR_INVALID

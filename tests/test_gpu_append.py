@@ -48,6 +48,7 @@ def run_append(fa, oracle, Hq, Hkv, d, T, pos0, max_ctx, base, neox, ff=None, de
     (40, 8, 128, 512, 7680, 1e6, 1),   # config 4: prefill chunk append
     (16, 16, 128, 9, 31, 1e4, 0),
     (40, 8, 128, 3, 0, 1e6, 1),
+    (8, 2, 64, 4, 100, 1e4, 0),        # d = 64 with interleaved pairs
 ])
 def test_rope_store_kv(gpu, oracle, Hq, Hkv, d, T, pos0, base, neox):
     run_append(gpu, oracle, Hq, Hkv, d, T, pos0, pos0 + T + 5, base, neox, seed=pos0 + T)
