@@ -76,6 +76,65 @@ def test_paged_matches_contiguous(gpu, oracle, nseq, lo, hi, Hq, Hkv, d):
         assert_close(as_f32(got[b]), oracle.decode(q[b], kc, vc, S, Hq, Hkv, d), f"seq {b} S={S}")
 
 
+def test_config5_exact_draw(gpu, oracle):
+    """benchmark config 5 exactly as bench.py draws it (seed 5): 16 sequences with S ~ U[256,
+    16384] (sum 117,916), 16-token pages at a seeded permutation of the pool; the one-launch
+    paged step (append at S-1 + decode) against the contiguous step of every sequence, bit
+    for bit, and the oracle."""
+    fa = gpu
+    B, Hq, Hkv, d, max_seq = 16, 40, 8, 128, 16384
+    kv_dim = Hkv * d
+    rng = np.random.default_rng(5)
+    lens = rng.integers(256, 16384 + 1, B).astype(np.int32)
+    assert int(lens.sum()) == 117916
+    nblk = [(int(s) + PAGE - 1) // PAGE for s in lens]
+    perm = rng.permutation(sum(nblk)).astype(np.int32)
+    data = np.random.default_rng(55)
+    table = np.full((B, max_seq // PAGE), -1, np.int32)
+    k_pool = np.zeros((sum(nblk), PAGE, kv_dim), np.uint16)
+    v_pool = np.zeros_like(k_pool)
+    seqs, at = [], 0
+    for b, S in enumerate(lens):
+        kc, vc = f16(data, (int(S), kv_dim)), f16(data, (int(S), kv_dim))
+        seqs.append((kc, vc))
+        for j in range(nblk[b]):
+            table[b, j] = perm[at]
+            rows = slice(j * PAGE, min(int(S), (j + 1) * PAGE))
+            k_pool[perm[at], :rows.stop - rows.start] = kc[rows]
+            v_pool[perm[at], :rows.stop - rows.start] = vc[rows]
+            at += 1
+    q, kn, vn = f16(data, (B, Hq * d)), f16(data, (B, kv_dim)), f16(data, (B, kv_dim))
+    rope = fa.rope_table_host(max_seq, d, 1e6)
+    drope = fa.DeviceBuffer.from_array(rope)
+    dq, dk, dv = (fa.DeviceBuffer.from_array(a) for a in (q, kn, vn))
+    dkp, dvp = fa.DeviceBuffer.from_array(k_pool), fa.DeviceBuffer.from_array(v_pool)
+    dt, dl = fa.DeviceBuffer.from_array(table), fa.DeviceBuffer.from_array(lens)
+    out = fa.DeviceBuffer(q.nbytes)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(B, Hq, max_seq))
+    fa.decodeWorkspaceInit(ws)
+    fa.pagedDecodeStep(dq, dk, dv, dkp, dvp, out, dt, table.shape[1], dl, B, max_seq, Hq, Hkv, d, drope, 1, ws)
+    fa.Hip.sync()
+    got = out.download((B, Hq * d), np.uint16)
+    for b, S in enumerate(int(x) for x in lens):
+        kc, vc = seqs[b]
+        # the contiguous one-launch step over the same rows (its row S-1 is overwritten by the append)
+        c = {n: fa.DeviceBuffer.from_array(a) for n, a in dict(q=q[b:b + 1], k=kn[b:b + 1], v=vn[b:b + 1], kc=kc,
+                                                                 vc=vc).items()}
+        cout = fa.DeviceBuffer(Hq * d * 2)
+        cws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_seq))
+        fa.decodeWorkspaceInit(cws)
+        cpos = fa.DeviceBuffer.from_array(np.array([S - 1], np.int32))
+        fa.decodeStep(c["q"], c["k"], c["v"], c["kc"], c["vc"], cout, cpos, 0, max_seq, Hq, Hkv,
+                      d, drope, 1, cws)
+        fa.Hip.sync()
+        assert np.array_equal(got[b], cout.download(Hq * d, np.uint16)), f"seq {b} (S={S}) differs from the contiguous step"
+        if b % 5 == 0:  # the oracle at a third of the sequences (the contiguous step is checked against it elsewhere)
+            qr, kr = q[b:b + 1].copy(), kn[b:b + 1].copy()
+            kc2, vc2 = kc.copy(), vc.copy()
+            oracle.rope_append(qr, kr, vn[b:b + 1], kc2, vc2, rope, S - 1, Hq, Hkv, d, 1)
+            assert_close(as_f32(got[b]), oracle.decode(qr[0], kc2, vc2, S, Hq, Hkv, d), f"config 5 seq {b} S={S}")
+
+
 def test_paged_append_then_decode(gpu, oracle):
     """Append one token per sequence through the block table, then decode; caches bit-exact."""
     fa = gpu

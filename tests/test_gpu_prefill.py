@@ -66,7 +66,7 @@ def test_other_shapes(gpu, oracle, Hq, Hkv, d, T, p0, q8):
     assert_close(got, ref, f"prefill {Hq}/{Hkv} d{d} T={T} p0={p0} q8={q8}")
 
 
-@pytest.mark.parametrize("p0", [0, 1024])
+@pytest.mark.parametrize("p0", [0, 1024, 7680])
 def test_config4_chunk_q8(gpu, oracle, p0):
     """Config 4 on an int8 cache: sampled rows vs the int8 decode oracle at S = p0 + t + 1."""
     fa = gpu
@@ -99,7 +99,7 @@ def test_q8_scales_off_dword_alignment(gpu, oracle):
     assert_close(got, oracle.prefill_q8(q, k, ks, v, vs, T, p0, Hq, Hkv, d), "prefill q8 misaligned scales")
 
 
-@pytest.mark.parametrize("p0", [0, 1024, 7680])
+@pytest.mark.parametrize("p0", [0, 1024, 2048, 4096, 7680])  # every p0 bench.py measures
 def test_config4_chunk(gpu, oracle, p0):
     """benchmark config 4: 40q/8kv d128, 512-token chunk after p0 cached tokens; sampled rows vs decode oracle."""
     fa = gpu
