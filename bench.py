@@ -44,7 +44,7 @@ MALL_BYTES = 256 << 20         # Infinity Cache: a "cold" working set must excee
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs recorded in the profile below (KiB per
 # dispatch, scaled by the copy-kernel calibration FETCH_SIZE x 2.0, WRITE_SIZE x 1.0);
 # it is not measured in this run.
-HEADLINE_TRAFFIC_BYTES = 135924531
+HEADLINE_TRAFFIC_BYTES = 135853839
 TRAFFIC_SOURCE = "constant from profiles/decode_step_cfg3_pmc.txt (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)"
 
 
@@ -597,8 +597,9 @@ def main():
                     help="only copy 1 GiB three times with the bench-kit streaming copy (one 16-byte load and "
                          "store per element): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run give the "
                          "counters' reading for a known 1 GiB read + 1 GiB write")
-    ap.add_argument("--config", choices=("headline", "all", "others", "prefill", "paged", "q8", "gemm", "layer", "append"), default="headline",
-                    help="headline: the driver's one line; all/others: also (only) the other benchmark configs of BASELINE.json")
+    ap.add_argument("--config", choices=("headline", "all", "others", "short", "prefill", "paged", "q8", "gemm", "layer", "append"), default="headline",
+                    help="headline: the driver's one line; all/others: also (only) the other benchmark configs of BASELINE.json; "
+                         "short: configs 1 and 2 only")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -618,30 +619,28 @@ def main():
         return
     if args.config in ("headline", "all"):
         print(json.dumps(headline(cx, args)), flush=True)
-    if args.config in ("all", "others"):
-        lines = [decode_config(cx, "1: Qwen2.5-0.5B layer", 513, 24, 14, 2, 64, args.steps, args.warmup, False)]
+    if args.config in ("all", "others", "short"):
+        emit = lambda rec: print(json.dumps(rec), flush=True)
+        emit(decode_config(cx, "1: Qwen2.5-0.5B layer", 513, 24, 14, 2, 64, args.steps, args.warmup, False))
         for S in (1024, 4096, 8192):
             for cold in (True, False):
-                lines.append(decode_config(cx, "2: 32q/8kv x 32 layers", S, 32, 32, 8, 128, args.steps, args.warmup,
-                                           cold))
-        lines.append(decode_config(cx, "3: 40q/8kv x 64 layers", 16384, 64, 40, 8, 128, args.steps, args.warmup,
-                                   False))
+                emit(decode_config(cx, "2: 32q/8kv x 32 layers", S, 32, 32, 8, 128, args.steps, args.warmup, cold))
+    if args.config in ("all", "others"):
+        emit(decode_config(cx, "3: 40q/8kv x 64 layers", 16384, 64, 40, 8, 128, args.steps, args.warmup, False))
         for p0 in (0, 1024, 2048, 4096, 7680):
-            lines.append(prefill_config(cx, p0, args.steps, args.warmup))
+            emit(prefill_config(cx, p0, args.steps, args.warmup))
         for p0 in (0, 7680):
-            lines.append(prefill_config(cx, p0, args.steps, args.warmup, q8=True))
-        lines.append(paged_config(cx, args.steps, args.warmup))
+            emit(prefill_config(cx, p0, args.steps, args.warmup, q8=True))
+        emit(paged_config(cx, args.steps, args.warmup))
         for T in (1, 512):
-            lines.append(append_config(cx, T, args.steps, args.warmup))
-        lines.append(q8_config(cx, 32768, 64, args.steps, args.warmup))
+            emit(append_config(cx, T, args.steps, args.warmup))
+        emit(q8_config(cx, 32768, 64, args.steps, args.warmup))
         for case in GEMM_CASES:
-            lines.append(gemm_config(cx, *case, args.steps, args.warmup))
+            emit(gemm_config(cx, *case, args.steps, args.warmup))
         for case in GEMV_CASES:
-            lines.append(gemv_config(cx, *case, args.steps, args.warmup))
-        lines.append(layer_block_config(cx, 32768, 64, args.steps, args.warmup))
-        lines.append(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True))
-        for rec in lines:
-            print(json.dumps(rec), flush=True)
+            emit(gemv_config(cx, *case, args.steps, args.warmup))
+        emit(layer_block_config(cx, 32768, 64, args.steps, args.warmup))
+        emit(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True))
     if args.config == "q8":
         print(json.dumps(q8_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
     if args.config == "append":

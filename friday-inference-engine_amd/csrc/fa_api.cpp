@@ -80,9 +80,10 @@ int env_int(const char* name, int dflt, int lo, int hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// Workspace: arrival counters [B*Hq], one int per 256 bytes, at offset 0 (the fused
-// merge uses B*Hkv*ceil(G/16) <= B*Hq of them; they must stay at a fixed place
-// whatever the split count of a call), then part_o [B*Hq][ns][d] fp32 and
+// Workspace: arrival counter slots [B*Hq], 256 bytes each, at offset 0 (the fused
+// merge uses B*Hkv*ceil(G/16) <= B*Hq of them, each an arrival count and the base it had
+// when the last launch completed; they must stay at a fixed place whatever the split
+// count of a call), then part_o [B*Hq][ns][d] fp32 and
 // part_ml [B*Hq][ns][2].
 size_t counters_bytes(int batch, int Hq) { return (size_t)batch * Hq * fa::kCounterStride * sizeof(int); }
 
@@ -336,7 +337,8 @@ ScratchSlot g_scratch[64];
 
 // The device address of the current device's scratch (the host-side name `scratch` is not
 // one), looked up once per device; the first call also zeroes it with a fill kernel on
-// `stream` (the counters must start at zero; every call leaves them at zero).
+// `stream` (counter and base start equal; every completed call advances both by the same
+// amount, so they stay consistent).
 void* scratch_ptr(hipStream_t stream, hipError_t* err) {
     int dev = 0;
     if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;

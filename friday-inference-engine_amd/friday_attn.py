@@ -325,7 +325,7 @@ def decodeWorkspaceInit(workspace, workspace_bytes=None, stream=None):
 
 def launchDecodeAttentionFused(q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads, num_kv_heads,
                                head_dim, workspace, stream=None, k_scale=None, v_scale=None, workspace_bytes=None):
-    """Split-K decode with the merge done by the last workgroup (one kernel)."""
+    """Split-K decode with the merge done inside the same kernel by the last-dispatched splits."""
     if workspace_bytes is None:
         workspace_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else 0
     _check(load().friday_attn_decode_attention_fused(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), seq_len,

@@ -107,11 +107,13 @@ int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, c
 
 /* Zeroes a decode workspace (a small fill kernel, no hipMemset node). Required once,
  * after allocation, before the workspace is used by friday_attn_decode_attention_fused
- * or friday_attn_paged_decode_attention; those calls leave it ready for the next call. */
+ * or friday_attn_paged_decode_attention; those calls leave it ready for the next call
+ * (each group's arrival counter and its base advance together, nothing is reset). */
 int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 /* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
- * workgroup of each kv head to finish (an arrival counter in the workspace) instead of
- * by a second kernel. Same arguments, same results bit for bit as
+ * few workgroups of each kv head (the ones dispatched last), each over a slice of the
+ * columns, once an arrival counter in the workspace shows every split stored, instead
+ * of by a second kernel. Same arguments, same results bit for bit as
  * friday_attn_decode_attention_split; the workspace must have been initialised with
  * friday_attn_decode_workspace_init. Calls that share a workspace must not overlap. */
 int friday_attn_decode_attention_fused(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out,
