@@ -31,11 +31,15 @@ constexpr int kTile = 16;  // positions per wave tile
 constexpr int kStages = 1;    // register stages (tiles in flight) per wave
 // int8 rows are half as wide: twice the tiles in flight keep the same bytes in flight
 constexpr int kStagesQ8 = 2;
-constexpr int kShortStages = 4;
+constexpr int kShortStages = 4;  // stages when a wave has at most this many tiles
 constexpr int kMergeSlices = 8;  // column slices of the distributed fused merge
-constexpr float kLazy2 = 8.0f;   // lazy softmax reference: rescale when a max rises by > 2^8            // stages when a wave has at most this many tiles
+constexpr size_t kResidentWorkgroups = 512;  // two workgroups per CU on the 256 CUs of an MI355X
+constexpr float kLazy2 = 8.0f;   // lazy softmax reference: rescale when a max rises by > 2^8
 
-template <int D, bool Q8>
+// ALIAS: the wave combine reuses the tile region (after a barrier), so that two workgroups
+// fit in a CU's LDS with room to spare; used by the paged kernel, whose grids hold many
+// workgroups per CU. Otherwise the combine has a region of its own and needs no barrier.
+template <int D, bool Q8, bool ALIAS>
 struct Geo {
     static constexpr int LROW = D * 2 + 16;           // LDS row stride in bytes (fp16 row + 16 B pad)
     static constexpr int KSTEPS = D / 32;             // MFMA k-steps over the head dimension
@@ -48,8 +52,10 @@ struct Geo {
     static constexpr int WAVE_LDS = 2 * kTile * LROW;  // K and V tile of one wave
     static constexpr int CROW = D + 4;                 // combine row stride in floats (bank spread)
     static constexpr int COMB_LDS = (2 * kWaves * 16 + kWaves * 16 * CROW) * 4;
-    static constexpr int QX_OFF = kWaves * WAVE_LDS + COMB_LDS;  // rotated q rows, 16 heads x D fp16
-    static constexpr int LDS = QX_OFF + 16 * D * 2;              // tiles, the wave combine, the q rows
+    static constexpr int TILES = kWaves * WAVE_LDS;
+    static constexpr int COMB_OFF = ALIAS ? 0 : TILES;
+    static constexpr int QX_OFF = ALIAS ? (TILES > COMB_LDS ? TILES : COMB_LDS) : TILES + COMB_LDS;  // rotated q rows
+    static constexpr int LDS = QX_OFF + 16 * D * 2;  // tiles, the wave combine, the q rows (16 heads x D fp16)
 };
 
 __device__ __forceinline__ int context_len(const DecodeParams& p, int b, bool paged) {
@@ -267,7 +273,7 @@ __device__ __forceinline__ void wait_count(const unsigned* cnt, unsigned target)
 template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
 // two workgroups per CU (two waves per SIMD) must fit: a 256-register budget
 __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) {
-    using Gm = Geo<D, Q8>;
+    using Gm = Geo<D, Q8, PAGED>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
 
     // grid x = (kv head, head block) group, y = split: consecutive workgroup ids walk the
@@ -293,14 +299,16 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
                                : split_chunk(S, p.min_chunk, p.max_splits);
     const int nsp = p.single ? 1 : split_count(S, p.min_chunk, p.max_splits);
     if (split >= nsp) return;  // inactive split; the merge ignores it
-    // fused merge (see the end of the kernel): this workgroup's merge slice (mk >= 0 for the
-    // last nslice splits) and, for mergers, the group's counter base, loaded early
-    const int nslice = (nsp > 1 && p.counters) ? merge_slices<D>(p, nsp) : 1;
+    // fused merge (see the end of the kernel): in the fixed-merger form, this workgroup's
+    // merge slice (mk >= 0 for the last nslice splits); the group's counter base, loaded
+    // early by the workgroups that need it (mergers, or every one in the last-arriver form)
+    const bool last_arriver = p.merge_slices == 0;
+    const int nslice = (nsp > 1 && p.counters && !last_arriver) ? merge_slices<D>(p, nsp) : 1;
     const int mk = split - (nsp - nslice);
     // (grid x = Hkv * ngb groups)
     unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)b * p.Hkv * p.ngb + group) * kCounterStride;
     unsigned base = 0;
-    if (nsp > 1 && p.counters && mk >= 0)
+    if (nsp > 1 && p.counters && (mk >= 0 || last_arriver))
         base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
@@ -492,51 +500,50 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         float ks[Gm::NLD], vs[Gm::NLD];
     };
 
-    // Contiguous caches: each tile is read through buffer descriptors that cover exactly its
-    // rows inside [start, end), so rows past the end, and whole tiles past the last one (the
-    // refill after a wave's last tile), read as zeros without touching memory; the lane's
-    // byte offsets are the same for every tile. Paged pools go through the block table, rows
-    // clamped to the split and a tile past the end reading this workgroup's q row instead.
-    const char* qrow_bytes = reinterpret_cast<const char*>(p.q + (size_t)b * p.Hq * D + (size_t)kvh * p.G * D);
+    // Each tile is read through buffer descriptors that cover exactly its rows inside
+    // [start, end), so rows past the end, and whole tiles past the last one (the refill after
+    // a wave's last tile), read as zeros without touching memory; the lane's byte offsets are
+    // the same for every tile. Paged pools: a tile is one page (splits start at multiples of
+    // 128 positions), found through the block table. The pages of this wave's first 64 tiles
+    // (tiles wave + 4 i) are loaded once, one per lane, and taken with a lane read per tile.
+    static_assert(kTile == kPageTokens, "one page per tile");
+    int wpages = 0;
+    if constexpr (PAGED) {
+        const int pt = start + (wave + kWaves * lane) * kTile;
+        wpages = pt < end ? p.block_table[(size_t)b * p.bt_stride + (pt >> 4)] : 0;
+    }
     const uint32_t lane_off = (uint32_t)(lrow * rowb + lchunk * 16);
     const uint32_t srow = (uint32_t)(p.kv_dim / 32) * 2;  // bytes of one position's int8 scales
     const uint32_t lane_soff = (uint32_t)lrow * srow + (uint32_t)(lchunk * 16 / 32) * 2;
     auto load_tile = [&](Stage& st, int t) {
         const int base = start + t * kTile;
-        if constexpr (!PAGED) {
-            const uint32_t nrows = (uint32_t)min(max(end - base, 0), kTile);
-            const __amdgpu_buffer_rsrc_t rk = uniform_rsrc(kbase + (size_t)base * rowb, nrows * (uint32_t)rowb);
-            const __amdgpu_buffer_rsrc_t rv = uniform_rsrc(vbase + (size_t)base * rowb, nrows * (uint32_t)rowb);
+        const uint32_t nrows = (uint32_t)min(max(end - base, 0), kTile);
+        size_t row0 = (size_t)base;  // cache row of the tile's first position
+        if constexpr (PAGED) {
+            const int li = (t - wave) / kWaves;  // this wave's tile number (uniform)
+            int phys;
+            if (li < 64)
+                phys = __builtin_amdgcn_readlane(wpages, li);
+            else
+                phys = nrows ? __builtin_amdgcn_readfirstlane(p.block_table[(size_t)b * p.bt_stride + (base >> 4)]) : 0;
+            row0 = (size_t)phys * kPageTokens;
+        }
+        const __amdgpu_buffer_rsrc_t rk = uniform_rsrc(kbase + row0 * rowb, nrows * (uint32_t)rowb);
+        const __amdgpu_buffer_rsrc_t rv = uniform_rsrc(vbase + row0 * rowb, nrows * (uint32_t)rowb);
+#pragma unroll
+        for (int r = 0; r < Gm::NLD; ++r) {
+            st.k[r] = ld_buf_nt(rk, lane_off + (uint32_t)(r * Gm::RPI) * (uint32_t)rowb);
+            st.v[r] = ld_buf_nt(rv, lane_off + (uint32_t)(r * Gm::RPI) * (uint32_t)rowb);
+        }
+        if constexpr (Q8) {
+            static_assert(!PAGED, "int8 pages are not supported");
+            const size_t sb = (size_t)base * (p.kv_dim / 32) + (size_t)kvh * (D / 32);
+            const __amdgpu_buffer_rsrc_t rks = uniform_rsrc(p.k_scale + sb, nrows * srow);
+            const __amdgpu_buffer_rsrc_t rvs = uniform_rsrc(p.v_scale + sb, nrows * srow);
 #pragma unroll
             for (int r = 0; r < Gm::NLD; ++r) {
-                st.k[r] = ld_buf_nt(rk, lane_off + (uint32_t)(r * Gm::RPI) * (uint32_t)rowb);
-                st.v[r] = ld_buf_nt(rv, lane_off + (uint32_t)(r * Gm::RPI) * (uint32_t)rowb);
-            }
-            if constexpr (Q8) {
-                const size_t sb = (size_t)base * (p.kv_dim / 32) + (size_t)kvh * (D / 32);
-                const __amdgpu_buffer_rsrc_t rks = uniform_rsrc(p.k_scale + sb, nrows * srow);
-                const __amdgpu_buffer_rsrc_t rvs = uniform_rsrc(p.v_scale + sb, nrows * srow);
-#pragma unroll
-                for (int r = 0; r < Gm::NLD; ++r) {
-                    st.ks[r] = ld_buf_f16(rks, lane_soff + (uint32_t)(r * Gm::RPI) * srow);
-                    st.vs[r] = ld_buf_f16(rvs, lane_soff + (uint32_t)(r * Gm::RPI) * srow);
-                }
-            }
-        } else {
-            const bool past = t >= ntiles;  // uniform
-            const char* kb = past ? qrow_bytes : kbase;
-            const char* vb = past ? qrow_bytes : vbase;
-#pragma unroll
-            for (int r = 0; r < Gm::NLD; ++r) {
-                const int pos = base + r * Gm::RPI + lrow;
-                const size_t ri = past ? 0 : row_index<PAGED>(p, b, max(min(pos, end - 1), start));
-                st.k[r] = ld_nt(reinterpret_cast<const u4*>(kb + ri * rowb) + lchunk);
-                st.v[r] = ld_nt(reinterpret_cast<const u4*>(vb + ri * rowb) + lchunk);
-                if (Q8) {
-                    const size_t si = (ri * p.kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
-                    st.ks[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
-                    st.vs[r] = (float)*reinterpret_cast<const _Float16*>(p.v_scale + si);
-                }
+                st.ks[r] = ld_buf_f16(rks, lane_soff + (uint32_t)(r * Gm::RPI) * srow);
+                st.vs[r] = ld_buf_f16(rvs, lane_soff + (uint32_t)(r * Gm::RPI) * srow);
             }
         }
     };
@@ -551,11 +558,10 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
 #pragma unroll
             for (int r = 0; r < Gm::NLD; ++r) {
                 const int row = r * Gm::RPI + lrow;
-                const bool live = tbase + row < end;
-                ck[r] = st.k[r];
+                ck[r] = st.k[r];  // zeros past the end
                 cv[r] = st.v[r];
-                sk[r] = (!PAGED || live) ? st.ks[r] : 0.0f;  // contiguous: zeros past the end already
-                sv[r] = (!PAGED || live) ? st.vs[r] : 0.0f;
+                sk[r] = st.ks[r];
+                sv[r] = st.vs[r];
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
                     ck[r] = kq;  // the new row, as quantized and written to the cache by this wave
                     cv[r] = vq;
@@ -578,13 +584,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
         } else {
-            // registers -> wave-private LDS tile (rows past the end as zeros)
+            // registers -> wave-private LDS tile (rows past the end are zeros)
 #pragma unroll
             for (int r = 0; r < Gm::NLD; ++r) {
                 const int row = r * Gm::RPI + lrow;
-                const bool live = tbase + row < end;
-                const u4 z = u4{0, 0, 0, 0};
-                u4 kx = (!PAGED || live) ? st.k[r] : z, vx = (!PAGED || live) ? st.v[r] : z;  // contiguous: zeros already
+                u4 kx = st.k[r], vx = st.v[r];
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
                     kx = rk;  // the new row, as written to the cache by this wave
                     vx = *reinterpret_cast<const u4*>(&nv[0]);
@@ -595,7 +599,7 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
             // Refill this stage while computing. Unconditional, so no branch hides loads from
-            // the wait counter: a tile past the end reads this wave's q row instead.
+            // the wait counter (a tile past the end reads nothing and gives zeros).
             load_tile(st, t_next);
         }
         if (t >= ntiles) return;  // uniform: this stage held no tile
@@ -679,9 +683,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
         stream(std::integral_constant<int, NST>{});
 
     // ---- combine the four waves of the workgroup through LDS ----
-    // (each wave writes its state into a region of its own, so no barrier is needed before)
+    // (with a region of its own, each wave writes its state without waiting for the others;
+    // over the tiles, every wave must be done reading its tiles first)
     l_run = col_sum4(l_run);
-    float* cm = reinterpret_cast<float*>(smem + kWaves * Gm::WAVE_LDS);  // [kWaves][16]
+    if constexpr (Gm::COMB_OFF == 0) __syncthreads();
+    float* cm = reinterpret_cast<float*>(smem + Gm::COMB_OFF);  // [kWaves][16]
     float* cl = cm + kWaves * 16;                          // [kWaves][16]
     float* co = cl + kWaves * 16;                          // [kWaves][16][CROW]
     if (kb == 0) {
@@ -737,18 +743,35 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
     if (nsp == 1) write_q();
 
     // Fused merge. Every workgroup of this (sequence, kv head, head block) adds 1 to the
-    // group's arrival counter once its partials are stored, and does not wait for the
-    // atomic. The counter is never reset: a launch is complete when it has grown by nsp
-    // over the group's base, which merger 0 then advances by nsp for the next launch.
-    // The mergers are the last nslice splits of the group, i.e. the workgroups dispatched
-    // last (workgroups are dispatched in increasing id order): each waits until the
-    // counter is complete, which only needs workgroups dispatched before it, then merges
-    // its column slice. Merger 0 also writes the rotated q back and advances the base.
+    // group's arrival counter once its partials are stored. The counter is never reset: a
+    // launch is complete when it has grown by nsp over the group's base, which the
+    // workgroup that merges (merger 0) then advances by nsp for the next launch.
+    // Fixed-merger form (grids that fit on the device at once): nobody waits for the
+    // atomic. The mergers are the last nslice splits of the group, i.e. the workgroups
+    // dispatched last (workgroups are dispatched in increasing id order): each waits until
+    // the counter is complete, which only needs workgroups dispatched before it, then
+    // merges its column slice. Merger 0 also writes the rotated q back.
+    // Last-arriver form (larger grids, where a waiting merger would hold a slot that
+    // later workgroups need): the atomic returns the count before this arrival, and the
+    // workgroup that completes the count merges every column.
     if (nsp > 1 && p.counters) {
         // The partials were written through to the device coherence point (sc1 stores);
         // wait until every one of them has completed before this workgroup is counted.
         wait_vmem();
         __syncthreads();
+        if (last_arriver) {
+            __shared__ int is_last;
+            if (tid == 0)
+                is_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - base ==
+                          (unsigned)nsp - 1u;
+            __syncthreads();
+            if (!is_last) return;
+            merge_any<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp);
+            write_q();  // every workgroup of the group has read q by now
+            if (tid == 0) __hip_atomic_store(cnt + kCounterStride / 2, base + (unsigned)nsp, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
         if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (mk < 0) return;
         if (tid == 0) wait_count(cnt, base + (unsigned)nsp);
@@ -776,7 +799,9 @@ template <int D, bool PAGED, bool Q8>
 int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
-    p.merge_slices = kMergeSlices;
+    // fixed mergers while the whole grid can be resident (two workgroups per CU on 256
+    // CUs), else the last arriver merges
+    p.merge_slices = (size_t)grid.x * grid.y * grid.z <= kResidentWorkgroups ? kMergeSlices : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
         hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid, dim3(kThreads), 0, stream, p);

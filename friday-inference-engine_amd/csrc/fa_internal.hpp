@@ -63,7 +63,7 @@ struct DecodeParams {
     int Hq, Hkv, G, ngb, nsplit_grid, kv_dim;
     int single;                // 1: one split covers the whole context, no merge
     int min_chunk, max_splits; // split partition constants
-    int merge_slices;          // fused merge spread over up to this many arrivals (set by the launcher)
+    int merge_slices;          // fused merge: column slices over the last splits, 0 = the last arriver merges (set by the launcher)
     float scale2;              // softmax scale * log2(e)
     // fused RoPE + KV append (decode step): the kernel rotates q itself, the
     // workgroup owning position S-1 rotates k and writes the new K/V row, and the
