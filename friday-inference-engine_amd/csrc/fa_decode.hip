@@ -32,8 +32,13 @@ constexpr int kStages = 1;    // register stages (tiles in flight) per wave
 // int8 rows are half as wide: twice the tiles in flight keep the same bytes in flight
 constexpr int kStagesQ8 = 2;
 constexpr int kShortStages = 4;  // stages when a wave has at most this many tiles
+// Paged grids hold several workgroups per CU: three per CU (at most 168 registers), and at
+// most two tiles in flight per wave in the short-split form, where four made the waves of a
+// CU issue their loads in one burst and then wait together.
+constexpr int kPagedWgsPerCu = 3;
+constexpr int kShortStagesPaged = 2;
 constexpr int kMergeSlices = 8;  // column slices of the distributed fused merge
-constexpr size_t kResidentWorkgroups = 512;  // two workgroups per CU on the 256 CUs of an MI355X
+constexpr size_t kCus = 256;  // compute units of an MI355X
 constexpr float kLazy2 = 8.0f;   // lazy softmax reference: rescale when a max rises by > 2^8
 
 // ALIAS: the wave combine reuses the tile region (after a barrier), so that two workgroups
@@ -271,8 +276,8 @@ __device__ __forceinline__ void wait_count(const unsigned* cnt, unsigned target)
 }
 
 template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
-// two workgroups per CU (two waves per SIMD) must fit: a 256-register budget
-__global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) {
+// two workgroups per CU (two waves per SIMD) must fit: a 256-register budget; paged: three
+__global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decode_kernel(DecodeParams p) {
     using Gm = Geo<D, Q8, PAGED>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
 
@@ -677,8 +682,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa_decode_kernel(DecodeParams p) 
             }
         }
     };
-    if ((ntiles + kWaves - 1) / kWaves <= kShortStages)
-        stream(std::integral_constant<int, kShortStages>{});
+    constexpr int kShort = PAGED ? kShortStagesPaged : kShortStages;
+    if ((ntiles + kWaves - 1) / kWaves <= kShort)
+        stream(std::integral_constant<int, kShort>{});
     else
         stream(std::integral_constant<int, NST>{});
 
@@ -799,9 +805,9 @@ template <int D, bool PAGED, bool Q8>
 int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
-    // fixed mergers while the whole grid can be resident (two workgroups per CU on 256
-    // CUs), else the last arriver merges
-    p.merge_slices = (size_t)grid.x * grid.y * grid.z <= kResidentWorkgroups ? kMergeSlices : 0;
+    // fixed mergers while the whole grid can be resident at once, else the last arriver merges
+    const size_t resident = kCus * (PAGED ? kPagedWgsPerCu : 2);
+    p.merge_slices = (size_t)grid.x * grid.y * grid.z <= resident ? kMergeSlices : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
         hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid, dim3(kThreads), 0, stream, p);
