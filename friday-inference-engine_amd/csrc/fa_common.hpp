@@ -130,16 +130,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
                                              0x00020000);
 }
 
-// Nontemporal buffer loads (cache policy nt): 16 bytes, and one fp16 value as a float.
+// Nontemporal buffer loads (cache policy nt): 16 bytes, and one fp16 value as its bits.
 // Offsets at or past the descriptor's byte count read as zero.
 constexpr int kCpolNt = 2;
 __device__ __forceinline__ u4 ld_buf_nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     const i4v x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCpolNt);
     return *reinterpret_cast<const u4*>(&x);
 }
-__device__ __forceinline__ float ld_buf_f16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-    const short x = __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, kCpolNt);
-    return (float)__builtin_bit_cast(_Float16, x);
+__device__ __forceinline__ short ld_buf_f16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, kCpolNt);
+}
+// Copies of loaded registers, made at this point of the program into registers other than
+// the source (early clobber). A pipeline stage that is copied out and then reloaded in
+// place keeps its loop-carried registers: left to itself, the compiler may load the refill
+// into fresh registers and move it back at the end of the loop iteration, which waits for
+// the refill right after issuing it. The fp16 form also keeps the compiler from repacking
+// or converting the loaded bits before this point.
+__device__ __forceinline__ uint32_t copy_here(uint32_t x) {
+    uint32_t y;
+    asm volatile("v_mov_b32 %0, %1" : "=&v"(y) : "v"(x));
+    return y;
+}
+__device__ __forceinline__ u4 copy_here(u4 x) {
+    return u4{copy_here(x[0]), copy_here(x[1]), copy_here(x[2]), copy_here(x[3])};
+}
+__device__ __forceinline__ _Float16 f16_bits_here(short x) {
+    return __builtin_bit_cast(_Float16, (short)copy_here((uint32_t)(uint16_t)x));
 }
 
 __device__ __forceinline__ void st_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f4 v) {
@@ -169,8 +185,8 @@ __device__ __forceinline__ T ld_nt(const T* p) {
 // q becomes the fp16 number 1664 + q by splicing (q ^ 0x80) under the exponent byte
 // 0x66 (v_perm), minus 1664 (exact), times the scale: one fp16 rounding of the exact
 // product, the same bits as rounding the fp32 product q * scale to fp16.
-__device__ __forceinline__ void dequant16(u4 raw, float sc, u4& lo, u4& hi) {
-    const h2 s2 = h2{(_Float16)sc, (_Float16)sc};  // sc is an fp16 value: exact
+__device__ __forceinline__ void dequant16(u4 raw, _Float16 sc, u4& lo, u4& hi) {
+    const h2 s2 = h2{sc, sc};
     const h2 bias = h2{(_Float16)1664.0f, (_Float16)1664.0f};
     uint32_t o[8];
 #pragma unroll

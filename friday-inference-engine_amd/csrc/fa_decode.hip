@@ -107,16 +107,6 @@ __device__ __forceinline__ void quant_chunk16(const h8* x, u4& q, float& scale, 
     bits = __builtin_bit_cast(uint16_t, dh);
 }
 
-// Log-sum-exp merge of the split partials of nh consecutive query-head rows
-// (row0 .. row0+nh-1) by the 256 threads of a workgroup, one thread per output
-// float4: M = max m_s, w_s = exp(m_s - M) (0 below -50),
-// out = sum_s w_s o_s / sum_s w_s l_s, NaN -> 0, clamp, fp16
-// (attention_kernels.cu:207-235). The sums run over s in increasing order for
-// every head, so the merge kernel (nh = 1) and the fused last-workgroup merge
-// (nh = heads of the group) give the same bits. Partials are read with loads that
-// bypass the caches: in the fused path other workgroups of this launch wrote them
-// through to memory just before.
-// NB: partial rows per thread loaded in one round trip (8 or 32, >= nsp when possible)
 // Writes 4 consecutive output values of one head row (columns 4c..4c+3) and, when the
 // caller asked for it, their int8 form: per 32 values d = amax / 127, q = clamp(rne(x / d)),
 // exactly as quantize_x_q8_kernel (hpc_k_quants.cu:386-400) applied to the fp16 output.
@@ -293,8 +283,19 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     pin_sgpr(p.Hkv); pin_sgpr(p.out_q); pin_sgpr(p.scale2); pin_sgpr(p.nsplit_grid);
     if (PAGED) { pin_sgpr(p.seq_lens); pin_sgpr(p.block_table); pin_sgpr(p.bt_stride); }
     if (ROPE) { pin_sgpr(p.rope_table); pin_sgpr(p.neox); pin_sgpr(p.k_new); pin_sgpr(p.v_new); }
-    const int group = blockIdx.x;
-    const int split = blockIdx.y;
+    // int8 caches: the block scales of one position, for all kv heads, share a cache line, so
+    // the workgroups of one split (every kv head group) are placed on one XCD (ids are dealt
+    // to the 8 XCDs in turn) to read those lines through one L2. Within a group the splits
+    // keep increasing with the id, as the fused merge requires.
+    int group = blockIdx.x, split = blockIdx.y;
+    if constexpr (Q8 && !PAGED) {
+        if ((gridDim.y & 7) == 0) {
+            const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+            const int r = lin >> 3;
+            group = r % gridDim.x;
+            split = (lin & 7) + 8 * (r / gridDim.x);
+        }
+    }
     const int kvh = group / p.ngb, gb = group % p.ngb;
     const int b = blockIdx.z;
     // context length: read once (the device position or sequence length), clamped to the cache
@@ -335,7 +336,8 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     // S-1. They are issued before the first K/V tile and used after it is in flight. A
     // chunk is the 16 bytes one lane moves per cache row: 8 fp16 values, or 16 int8 ones.
     constexpr int HD2 = D / 2;
-    constexpr int PPT = ROPE ? D / 32 : 1;  // q rotation pairs per thread (16 head columns x D/2 pairs)
+    constexpr int TPH = kThreads / 16;            // threads per head column in the q rotation
+    constexpr int PPT = ROPE ? HD2 / TPH : 1;     // q rotation pairs per thread (16 head columns x D/2 pairs)
     constexpr int CW = Q8 ? 16 : 8;                       // values of one row chunk
     constexpr int NH = ROPE ? CW / 8 : 1;                 // fp16 vectors of one row chunk
     _Float16 rq0[PPT], rq1[PPT];
@@ -370,8 +372,8 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         if constexpr (!ROPE) return;
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
-        if (rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / 16
-            const int hg = gb * 16 + (tid >> 4), i0 = (tid & 15) * PPT;
+        if (rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
+            const int hg = gb * 16 + tid / TPH, i0 = (tid % TPH) * PPT;
             const uint16_t* qr = p.q + ((size_t)b * p.Hq + kvh * p.G + (hg < p.G ? hg : 0)) * D;
 #pragma unroll
             for (int e = 0; e < PPT; ++e) {
@@ -408,11 +410,11 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     auto prepare = [&]() __attribute__((always_inline)) {
         if constexpr (ROPE) {
             if (rot_q) {
-                // The rotation of the group's q rows is spread over the 256 threads (thread t:
-                // rotation pairs i0 .. i0 + PPT - 1 of head column t / 16, from the values
+                // The rotation of the group's q rows is spread over the workgroup (thread t:
+                // rotation pairs i0 .. i0 + PPT - 1 of head column t / TPH, from the values
                 // load_inputs fetched), and every lane reads its rotated fragment back from LDS.
                 _Float16* qx = reinterpret_cast<_Float16*>(smem + Gm::QX_OFF);  // [16 heads][D]
-                const int hc = tid >> 4, i0 = (tid & 15) * PPT;
+                const int hc = tid / TPH, i0 = (tid % TPH) * PPT;
 #pragma unroll
                 for (int e = 0; e < PPT; ++e) {
                     if (p.neox)
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     const int lrow = lane / Gm::CPR, lchunk = lane % Gm::CPR;
     struct Stage {
         u4 k[Gm::NLD], v[Gm::NLD];
-        float ks[Gm::NLD], vs[Gm::NLD];
+        short ks[Gm::NLD], vs[Gm::NLD];  // int8 block scales (fp16 bits)
     };
 
     // Each tile is read through buffer descriptors that cover exactly its rows inside
@@ -559,19 +561,19 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
             // int8 rows: take the raw codes and scales out of the stage, refill it at once, and
             // dequantise into the wave's LDS tile while the refill is in flight
             u4 ck[Gm::NLD], cv[Gm::NLD];
-            float sk[Gm::NLD], sv[Gm::NLD];
+            _Float16 sk[Gm::NLD], sv[Gm::NLD];
 #pragma unroll
             for (int r = 0; r < Gm::NLD; ++r) {
                 const int row = r * Gm::RPI + lrow;
-                ck[r] = st.k[r];  // zeros past the end
-                cv[r] = st.v[r];
-                sk[r] = st.ks[r];
-                sv[r] = st.vs[r];
+                ck[r] = copy_here(st.k[r]);  // zeros past the end
+                cv[r] = copy_here(st.v[r]);
+                sk[r] = f16_bits_here(st.ks[r]);
+                sv[r] = f16_bits_here(st.vs[r]);
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
                     ck[r] = kq;  // the new row, as quantized and written to the cache by this wave
                     cv[r] = vq;
-                    sk[r] = ksc;
-                    sv[r] = vsc;
+                    sk[r] = (_Float16)ksc;  // fp16 values: exact
+                    sv[r] = (_Float16)vsc;
                 }
             }
             load_tile(st, t_next);

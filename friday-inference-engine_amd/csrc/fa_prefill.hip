@@ -480,7 +480,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                 const int rem = idx % (kP2KS * Rg::CPR);
                 const int r = rem / Rg::CPR, c = rem % Rg::CPR;
                 u4 lo, hi;
-                dequant16(q[b], sc[b], lo, hi);
+                dequant16(q[b], (_Float16)sc[b], lo, hi);  // sc[b] is an fp16 value: exact
                 unsigned char* row = stage0 + ts * Gm::STAGE_K + r * Gm::ROWB;
                 *reinterpret_cast<u4*>(row + (((2 * c) ^ (r % Gm::CPR)) * 16)) = lo;
                 *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ (r % Gm::CPR)) * 16)) = hi;
