@@ -167,12 +167,15 @@ __device__ __forceinline__ float max8(float v) {
 //   out = L > 1e-12 ? acc * (1 / L) : 0, NaN -> 0, clamp, fp16.
 // Eight lanes serve one (head, float4 column) unit straight from memory (sc1 loads,
 // coherent with the sc1 stores of the other workgroups): up to 32 splits cost each lane
-// 4 + 4 loads in one round trip, with no LDS and no barrier. The order of the arithmetic
+// 4 + 4 loads per unit, and the units of up to four passes of the workgroup are loaded in
+// one round trip, with no LDS and no barrier. The order of the arithmetic
 // does not depend on the column range or on which workgroup runs it, so the separate
 // merge kernel and the column slices of the fused merge give the same bits. cw must be a
 // power of two; with out_q, cw and c0 must be multiples of 8.
 template <int D>
 __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, int c0, int cw) {
+    constexpr int kUnitsPerPass = kThreads / 8;
+    constexpr int kBatch = 4;  // passes whose partials are loaded in one round trip
     const int tid = threadIdx.x, r = tid & 7;
     const int wunit = __builtin_amdgcn_readfirstlane(tid >> 6) * 8;  // first unit of this wave in a pass
     const uint32_t ng = (uint32_t)p.nsplit_grid;
@@ -180,52 +183,63 @@ __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, 
     const __amdgpu_buffer_rsrc_t rml = coherent_rsrc(p.part_ml, 0x7fffffff);
     const int lc = __builtin_ctz(cw);
     const int units = nh * cw;
-    for (int u0 = 0; u0 < units; u0 += kThreads / 8) {
-        if (u0 + wunit >= units) break;  // uniform: no unit left for this wave
-        const int uu = u0 + (tid >> 3);
-        const int u = min(uu, units - 1);  // lanes past the last unit repeat it
-        const int hh = u >> lc, c = c0 + (u & (cw - 1));
-        const uint32_t row = (uint32_t)(row0 + hh) * ng;
-        // splits r, r + 8, r + 16, r + 24 (all of them up to 32 splits) in one round trip
-        float2 ml[4];
-        f4 ov[4];
+    for (int b0 = 0; b0 < units; b0 += kBatch * kUnitsPerPass) {
+        if (b0 + wunit >= units) break;  // uniform: no unit left for this wave
+        // splits r, r + 8, r + 16, r + 24 (all of them up to 32 splits) of up to kBatch units
+        float2 ml[kBatch][4];
+        f4 ov[kBatch][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t j = (uint32_t)min(r + 8 * i, nsp - 1);
-            ml[i] = ld_coherent2(rml, (row + j) * 8);
-            ov[i] = ld_coherent4(ro, ((row + j) * D + 4 * (uint32_t)c) * 4);
+        for (int k = 0; k < kBatch; ++k) {
+            if (k > 0 && b0 + k * kUnitsPerPass + wunit >= units) break;  // uniform: no unit left for this wave
+            const int u = min(b0 + k * kUnitsPerPass + (tid >> 3), units - 1);  // lanes past the last unit repeat it
+            const uint32_t row = (uint32_t)(row0 + (u >> lc)) * ng;
+            const int c = c0 + (u & (cw - 1));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t j = (uint32_t)min(r + 8 * i, nsp - 1);
+                ml[k][i] = ld_coherent2(rml, (row + j) * 8);
+                ov[k][i] = ld_coherent4(ro, ((row + j) * D + 4 * (uint32_t)c) * 4);
+            }
         }
-        float M = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) M = fmaxf(M, r + 8 * i < nsp ? ml[i].x : -__builtin_inff());
-        for (int j0 = r + 32; j0 < nsp; j0 += 8)  // beyond 32 splits
-            M = fmaxf(M, ld_coherent2(rml, (row + (uint32_t)j0) * 8).x);
-        M = max8(M);
-        float L = 0.0f;
-        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < kBatch; ++k) {
+            if (b0 + k * kUnitsPerPass + wunit >= units) break;  // uniform
+            const int uu = b0 + k * kUnitsPerPass + (tid >> 3);
+            const int u = min(uu, units - 1);
+            const int hh = u >> lc, c = c0 + (u & (cw - 1));
+            const uint32_t row = (uint32_t)(row0 + hh) * ng;
+            float M = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float df = (r + 8 * i < nsp ? ml[i].x : -__builtin_inff()) - M;
-            const float w = df < kCut2 ? 0.0f : exp2_fast(df);
-            L += w * (r + 8 * i < nsp ? ml[i].y : 0.0f);
-            acc += w * ov[i];
+            for (int i = 0; i < 4; ++i) M = fmaxf(M, r + 8 * i < nsp ? ml[k][i].x : -__builtin_inff());
+            for (int j0 = r + 32; j0 < nsp; j0 += 8)  // beyond 32 splits
+                M = fmaxf(M, ld_coherent2(rml, (row + (uint32_t)j0) * 8).x);
+            M = max8(M);
+            float L = 0.0f;
+            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float df = (r + 8 * i < nsp ? ml[k][i].x : -__builtin_inff()) - M;
+                const float w = df < kCut2 ? 0.0f : exp2_fast(df);
+                L += w * (r + 8 * i < nsp ? ml[k][i].y : 0.0f);
+                acc += w * ov[k][i];
+            }
+            for (int j0 = r + 32; j0 < nsp; j0 += 8) {
+                const float2 m2 = ld_coherent2(rml, (row + (uint32_t)j0) * 8);
+                const f4 o2 = ld_coherent4(ro, ((row + (uint32_t)j0) * D + 4 * (uint32_t)c) * 4);
+                const float df = m2.x - M;
+                const float w = df < kCut2 ? 0.0f : exp2_fast(df);
+                L += w * m2.y;
+                acc += w * o2;
+            }
+            L = sum8(L);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = sum8(acc[i]);
+            const float inv = L > 1e-12f ? 1.0f / L : 0.0f;
+            h4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = out_half(acc[i] * inv);
+            store_out4(p, row0 + hh, D, c, o, uu < units && r == 0, 8);
         }
-        for (int j0 = r + 32; j0 < nsp; j0 += 8) {
-            const float2 m2 = ld_coherent2(rml, (row + (uint32_t)j0) * 8);
-            const f4 o2 = ld_coherent4(ro, ((row + (uint32_t)j0) * D + 4 * (uint32_t)c) * 4);
-            const float df = m2.x - M;
-            const float w = df < kCut2 ? 0.0f : exp2_fast(df);
-            L += w * m2.y;
-            acc += w * o2;
-        }
-        L = sum8(L);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = sum8(acc[i]);
-        const float inv = L > 1e-12f ? 1.0f / L : 0.0f;
-        h4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = out_half(acc[i] * inv);
-        store_out4(p, row0 + hh, D, c, o, uu < units && r == 0, 8);
     }
 }
 
