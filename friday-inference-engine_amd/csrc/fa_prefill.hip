@@ -280,6 +280,12 @@ struct P2Geo {
     static constexpr int DTILES = D / 16;
     static constexpr int OROW = D + 4;                 // combine row stride (floats)
     static constexpr int CREG_BYTES = 4 * (2 * kP2Slices * 16 + kP2Slices * 16 * OROW);  // one group's merge area
+    // LDS slot of 16-byte chunk c of row r: c ^ swz(r). swz is a bijection on r % CPR, so the
+    // K operand reads (16 consecutive rows, one chunk) hit 16 distinct slots; and the four
+    // rows a..a+3 (a % 4 == 0) of a V^T read get swz values that differ above bit 0, so their
+    // chunk pairs (2 dt, 2 dt + 1) land in 8 distinct slots (r % CPR alone gave 2-way
+    // bank conflicts there).
+    static __device__ __forceinline__ int swz(int r) { return ((r & (CPR / 2 - 1)) << 1) | ((r / (CPR / 2)) & 1); }
 };
 
 // int8 caches: raw stage = the codes of K and V (row-major, kP2KS rows of D bytes each)
@@ -403,7 +409,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
     for (int i = 0; i < CNI; ++i) {
         const int r = (wave * CNI + i) * CRPI + drow;
-        doff[i] = (uint32_t)(r * (int)rowb + (Q8 ? dslot : (dslot ^ (r % CCPR))) * 16);
+        doff[i] = (uint32_t)(r * (int)rowb + (Q8 ? dslot : (dslot ^ Gm::swz(r))) * 16);
     }
     lds_u8* const lds0 = (lds_u8*)(Q8 ? stage1 : stage0);
     lds_u8* const lds1 = (lds_u8*)(Q8 ? stage2 : stage1);
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
             for (int i = 0; i < CNI; ++i) {
                 const int r = (wave * CNI + i) * CRPI + drow;
-                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (Q8 ? dslot : (dslot ^ (r % CCPR))) * 16);
+                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (Q8 ? dslot : (dslot ^ Gm::swz(r))) * 16);
                 lds_u8* l = st + (wave * CNI + i) * CRPI * CROWB;
                 dma16(kt, off, l);
                 dma16(vt, off, l + VOFF);
@@ -482,8 +488,8 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                 u4 lo, hi;
                 dequant16(q[b], (_Float16)sc[b], lo, hi);  // sc[b] is an fp16 value: exact
                 unsigned char* row = stage0 + ts * Gm::STAGE_K + r * Gm::ROWB;
-                *reinterpret_cast<u4*>(row + (((2 * c) ^ (r % Gm::CPR)) * 16)) = lo;
-                *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ (r % Gm::CPR)) * 16)) = hi;
+                *reinterpret_cast<u4*>(row + (((2 * c) ^ Gm::swz(r)) * 16)) = lo;
+                *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ Gm::swz(r)) * 16)) = hi;
             }
         }
     };
@@ -512,7 +518,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                 const int r = wrow + mt * 16 + col;
 #pragma unroll
                 for (int s = 0; s < Gm::KSTEPS; ++s)
-                    ka[mt][s] = *reinterpret_cast<const h8*>(sk + r * Gm::ROWB + (((4 * s + kb) ^ (r % Gm::CPR)) * 16));
+                    ka[mt][s] = *reinterpret_cast<const h8*>(sk + r * Gm::ROWB + (((4 * s + kb) ^ Gm::swz(r)) * 16));
             }
             // phase 1: S^T for every row tile (independent MFMA chains, no branches)
             f4 sacc[N][2];
@@ -595,7 +601,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
                 for (int dt = 0; dt < Gm::DTILES; ++dt) {
                     const int d = dt * 16 + 4 * (col & 3);
-                    const unsigned char* a = sv + r * Gm::ROWB + (((d >> 3) ^ (r % Gm::CPR)) * 16) + (d & 7) * 2;
+                    const unsigned char* a = sv + r * Gm::ROWB + (((d >> 3) ^ Gm::swz(r)) * 16) + (d & 7) * 2;
                     const h4 lo = lds_read_tr16(a);
                     const h4 hi = lds_read_tr16(a + 16 * Gm::ROWB);
                     va[dt] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
