@@ -61,6 +61,11 @@ struct Geo {
     static constexpr int COMB_OFF = ALIAS ? 0 : TILES;
     static constexpr int QX_OFF = ALIAS ? (TILES > COMB_LDS ? TILES : COMB_LDS) : TILES + COMB_LDS;  // rotated q rows
     static constexpr int LDS = QX_OFF + 16 * D * 2;  // tiles, the wave combine, the q rows (16 heads x D fp16)
+    // LDS slot of the 16-byte chunk k (values 8k .. 8k+7) of a tile row. int8 rows: lane c
+    // dequantises chunks 2c and 2c+1 and writes them with two instructions; placing even
+    // chunks in slots 0 .. D/16-1 and odd ones after them makes each instruction's lanes of
+    // one row write 128 contiguous bytes (consecutive slots), free of bank conflicts.
+    static __device__ __forceinline__ int slot(int k) { return Q8 ? (k >> 1) + (k & 1) * (D / 16) : k; }
 };
 
 __device__ __forceinline__ int context_len(const DecodeParams& p, int b, bool paged) {
@@ -596,11 +601,11 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
                 const int row = r * Gm::RPI + lrow;
                 u4 lo, hi;
                 dequant16(ck[r], sk[r], lo, hi);
-                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32) = lo;
-                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 32 + 16) = hi;
+                *reinterpret_cast<u4*>(kl + row * Gm::LROW + Gm::slot(2 * lchunk) * 16) = lo;
+                *reinterpret_cast<u4*>(kl + row * Gm::LROW + Gm::slot(2 * lchunk + 1) * 16) = hi;
                 dequant16(cv[r], sv[r], lo, hi);
-                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32) = lo;
-                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 32 + 16) = hi;
+                *reinterpret_cast<u4*>(vl + row * Gm::LROW + Gm::slot(2 * lchunk) * 16) = lo;
+                *reinterpret_cast<u4*>(vl + row * Gm::LROW + Gm::slot(2 * lchunk + 1) * 16) = hi;
             }
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
@@ -629,7 +634,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < Gm::KSTEPS; ++s) {
-            const h8 a = *reinterpret_cast<const h8*>(kl + col * Gm::LROW + (s * 32 + kb * 8) * 2);
+            const h8 a = *reinterpret_cast<const h8*>(kl + col * Gm::LROW + Gm::slot(4 * s + kb) * 16);
             sacc = mfma16x16x32(a, qf[s], sacc);
         }
 
@@ -670,7 +675,8 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         // O^T += V^T P^T over the 16 positions (k = kb*4 + i); V^T by one transposing LDS read
 #pragma unroll
         for (int dt = 0; dt < Gm::DTILES; ++dt) {
-            const h4 va = lds_read_tr16(vl + (kb * 4 + (col >> 2)) * Gm::LROW + (dt * 16 + 4 * (col & 3)) * 2);
+            const h4 va = lds_read_tr16(vl + (kb * 4 + (col >> 2)) * Gm::LROW + Gm::slot(2 * dt + ((col & 3) >> 1)) * 16 +
+                                        (col & 1) * 8);
             o[dt] = mfma16x16x16(va, pf, o[dt]);
         }
         __builtin_amdgcn_wave_barrier();
