@@ -108,7 +108,10 @@ int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, c
 /* Zeroes a decode workspace (a small fill kernel, no hipMemset node). Required once,
  * after allocation, before the workspace is used by friday_attn_decode_attention_fused
  * or friday_attn_paged_decode_attention; those calls leave it ready for the next call
- * (each group's arrival counter and its base advance together, nothing is reset). */
+ * (each group's arrival counter and its base advance together, nothing is reset).
+ * A workspace is laid out for one batch size (batch * num_heads counter slots first, the
+ * split partials after them; a contiguous call counts as batch 1): calls with another
+ * batch size or head count may share it only after it is initialised again. */
 int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 /* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
  * few workgroups of each kv head (the ones dispatched last), each over a slice of the

@@ -199,3 +199,48 @@ def test_paged_empty_sequence(gpu, oracle):
         else:
             kc, vc = seqs[b]
             assert np.array_equal(got[b], contiguous_decode(fa, q[b], kc, vc, S, Hq, Hkv, d, max_seq)), f"seq {b}"
+
+
+def test_merge_forms_share_a_workspace(gpu):
+    """The two fused-merge forms advance each group's arrival counter and its base together.
+    Two paged calls on one workspace (same batch, so the same counter slots) alternate: long
+    sequences, whose grid exceeds the resident workgroups (the last arriver merges), and the
+    same sequences cut to 200 positions with max_seq_len 256 (192 workgroups: fixed mergers).
+    Every call is bit-identical to the same call on a fresh workspace, and the short one to
+    the separate merge kernel of the contiguous path."""
+    fa = gpu
+    Hq, Hkv, d, nseq = 40, 8, 128, 12
+    rng = np.random.default_rng(77)
+    kv_dim = Hkv * d
+    lens = [int(x) for x in rng.integers(3000, 9000, nseq)]
+    short = [min(s, 200) for s in lens]
+    max_seq = 9000
+    seqs, table, k_pool, v_pool = build_paged(rng, lens, kv_dim, max_seq)
+    q = f16(rng, (nseq, Hq * d))
+    dq = fa.DeviceBuffer.from_array(q)
+    dk, dv = fa.DeviceBuffer.from_array(k_pool), fa.DeviceBuffer.from_array(v_pool)
+    dt = fa.DeviceBuffer.from_array(table)
+    dl_long = fa.DeviceBuffer.from_array(np.array(lens, np.int32))
+    dl_short = fa.DeviceBuffer.from_array(np.array(short, np.int32))
+
+    def paged(ws, dl, ms):
+        out = fa.DeviceBuffer(q.nbytes)
+        fa.launchPagedDecodeAttention(dq, dk, dv, out, dt, table.shape[1], dl, nseq, ms, Hq, Hkv, d, ws)
+        fa.Hip.sync()
+        return out.download((nseq, Hq * d), np.uint16)
+
+    def fresh():
+        ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(nseq, Hq, max_seq))
+        fa.decodeWorkspaceInit(ws)
+        return ws
+
+    ref_long = paged(fresh(), dl_long, max_seq)
+    ref_short = paged(fresh(), dl_short, 256)
+    for b in (0, nseq - 1):
+        kc, vc = seqs[b]
+        assert np.array_equal(ref_short[b], contiguous_decode(fa, q[b], kc[:short[b]], vc[:short[b]], short[b], Hq, Hkv,
+                                                             d, 256)), f"seq {b}: paged short call differs"
+    shared = fresh()
+    for it in range(4):
+        assert np.array_equal(paged(shared, dl_long, max_seq), ref_long), f"long call {it} on the shared workspace differs"
+        assert np.array_equal(paged(shared, dl_short, 256), ref_short), f"short call {it} on the shared workspace differs"
