@@ -92,10 +92,12 @@ size_t split_ws_bytes(int batch, int Hq, int max_seq, int d) {
     return counters_bytes(batch, Hq) + (size_t)batch * Hq * ns * ((size_t)d + 2) * sizeof(float);
 }
 
-void set_workspace(fa::DecodeParams& p, void* ws, int batch, int d, bool fused) {
+// counter_region > 0: the partials start at that fixed offset instead of right after this
+// call's counter slots (a workspace shared by calls with different head counts).
+void set_workspace(fa::DecodeParams& p, void* ws, int batch, int d, bool fused, size_t counter_region = 0) {
     char* base = static_cast<char*>(ws);
     p.counters = fused ? reinterpret_cast<int*>(base) : nullptr;
-    p.part_o = reinterpret_cast<float*>(base + counters_bytes(batch, p.Hq));
+    p.part_o = reinterpret_cast<float*>(base + (counter_region ? counter_region : counters_bytes(batch, p.Hq)));
     p.part_ml = p.part_o + (size_t)batch * p.Hq * p.nsplit_grid * d;
 }
 
@@ -281,7 +283,7 @@ int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint
                        const void* v_layer, const uint16_t* k_scale, const uint16_t* v_scale, uint16_t* out,
                        const int* d_pos, int pos, int max_ctx, int num_heads, int num_kv_heads, int head_dim,
                        const float* rope_table, int neox, void* workspace, size_t workspace_bytes, void* stream,
-                       int8_t* out_q = nullptr, float* out_d = nullptr) {
+                       int8_t* out_q = nullptr, float* out_d = nullptr, size_t counter_region = 0) {
     if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
     if (!q || !k || !v || !k_layer || !v_layer || !out || !rope_table || max_ctx <= 0)
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
@@ -301,12 +303,17 @@ int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint
     p.rope_table = rope_table; p.k_new = k; p.v_new = v; p.neox = neox ? 1 : 0;
     const int grid_len = d_pos ? max_ctx : pos + 1;
     p.nsplit_grid = fa::split_bound(grid_len, p.min_chunk, p.max_splits);
-    const size_t need = split_ws_bytes(1, num_heads, grid_len, head_dim);
+    size_t need = split_ws_bytes(1, num_heads, grid_len, head_dim);
+    if (counter_region) {
+        if (counters_bytes(1, num_heads) > counter_region)
+            return fail(FA_ERR_WORKSPACE, "%s: %d heads exceed the counter region", w, num_heads);
+        need += counter_region - counters_bytes(1, num_heads);
+    }
     if (need >= (size_t(1) << 31))  // partials are addressed with 32-bit buffer offsets
         return fail(FA_ERR_UNSUPPORTED, "%s: split workspace beyond 2 GiB (%zu bytes)", w, need);
     if (!workspace || workspace_bytes < need)
         return fail(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)", w, need, workspace_bytes);
-    set_workspace(p, workspace, 1, head_dim, true);
+    set_workspace(p, workspace, 1, head_dim, true, counter_region);
     return launch_status(fa::launch_decode(p, head_dim, 1, false, q8, static_cast<hipStream_t>(stream)), w);
 }
 }  // namespace
@@ -321,11 +328,13 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
 
 namespace {
 // Device scratch of friday_attn_decode_step_noalloc: the arrival counters and split
-// partials that a caller's workspace holds otherwise. 4 MiB covers up to 4096 query heads
-// at d <= 128: at most 4096 partial rows of d + 2 floats (2.1 MB) plus one 256-byte
-// counter slot per head (1 MB). Every GPU the
-// library runs on holds its own copy until the process ends.
+// partials that a caller's workspace holds otherwise. The counters have a fixed region of
+// 1 MiB (one 256-byte slot per query head, up to 4096 heads) and the partials the 3 MiB
+// after it, whatever the head count of a call, so calls of models with different head
+// counts can share the scratch (each call leaves its counters equal to their bases). Every
+// GPU the library runs on holds its own copy until the process ends.
 constexpr size_t kScratchBytes = size_t(4) << 20;
+constexpr size_t kScratchCounterBytes = size_t(1) << 20;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 struct ScratchSlot {
@@ -365,15 +374,17 @@ int friday_attn_decode_step_noalloc(uint16_t* q, const uint16_t* k, const uint16
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
     if (!d_pos && (pos < 0 || pos >= max_ctx))
         return fail(FA_ERR_INVALID, "%s: position %d outside [0, %d)", w, pos, max_ctx);
-    const size_t need = split_ws_bytes(1, num_heads, d_pos ? max_ctx : pos + 1, head_dim);
-    if (need > kScratchBytes)
+    const size_t need = kScratchCounterBytes + (split_ws_bytes(1, num_heads, d_pos ? max_ctx : pos + 1, head_dim) -
+                                                counters_bytes(1, num_heads));
+    if (counters_bytes(1, num_heads) > kScratchCounterBytes || need > kScratchBytes)
         return fail(FA_ERR_WORKSPACE, "%s: needs %zu bytes of scratch, more than the %zu held per GPU", w, need,
                     kScratchBytes);
     hipError_t err = hipSuccess;
     void* ws = scratch_ptr(static_cast<hipStream_t>(stream), &err);
     if (!ws) return fail(FA_ERR_LAUNCH, "%s: device scratch unavailable: %s", w, hipGetErrorString(err));
     return decode_step_common(w, q, k, v, k_layer, v_layer, nullptr, nullptr, out, d_pos, pos, max_ctx, num_heads,
-                              num_kv_heads, head_dim, rope_table, neox, ws, kScratchBytes, stream);
+                              num_kv_heads, head_dim, rope_table, neox, ws, kScratchBytes, stream, nullptr, nullptr,
+                              kScratchCounterBytes);
 }
 
 int friday_attn_decode_step_q8(uint16_t* q, const uint16_t* k, const uint16_t* v, int8_t* k_layer,

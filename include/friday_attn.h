@@ -141,12 +141,12 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
 /* No counterpart in the reference. For callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
  * friday_attn_decode_step with the workspace replaced by a scratch the library holds in
- * device memory, 4 MiB per GPU (enough for up to 4096 query heads at head_dim <= 128).
- * Allocates nothing; the first call on a device looks the scratch up and zeroes it with a
- * fill kernel on `stream`. Results are bit-identical to friday_attn_decode_step. All calls
- * on one GPU share its scratch: calls that overlap (other streams, concurrent graph
- * replays) race and must be serialised by the caller. FA_ERR_WORKSPACE when the call
- * would need more than the 4 MiB. */
+ * device memory, 4 MiB per GPU: 1 MiB of counter slots (up to 4096 query heads) and 3 MiB
+ * of split partials. Allocates nothing; the first call on a device looks the scratch up and
+ * zeroes it with a fill kernel on `stream`. Results are bit-identical to
+ * friday_attn_decode_step. All calls on one GPU share its scratch, whatever their head
+ * counts: calls that overlap (other streams, concurrent graph replays) race and must be
+ * serialised by the caller. FA_ERR_WORKSPACE when the call would need more than that. */
 int friday_attn_decode_step_noalloc(uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* k_layer,
                                     uint16_t* v_layer, uint16_t* out, const int* d_pos, int pos, int max_ctx,
                                     int num_heads, int num_kv_heads, int head_dim, const float* rope_table, int neox,

@@ -1,7 +1,7 @@
 """friday_attn_decode_step_noalloc (the entry point that allocates nothing: its split
 counters and partials live in the library's per-GPU device scratch) against
 friday_attn_decode_step with a caller workspace: cache rows, rotated q and output bit for
-bit, on two calls in a row, the second with a smaller input. Argument checks need no GPU."""
+bit, on calls in a row with smaller inputs and other head counts. Argument checks need no GPU."""
 import ctypes as C
 
 import numpy as np
@@ -38,9 +38,13 @@ def run_pair(fa, Hq, Hkv, d, S, max_ctx, seed):
 @pytest.mark.gpu
 def test_noalloc_matches_workspace_step(gpu):
     # headline shape at 32k (32 splits, distributed merge), then a smaller call that
-    # reuses the scratch the first one left behind
+    # reuses the scratch the first one left behind; then a model with one query head per
+    # kv head (32 counter slots, more than the 14 heads of the call before it) and the
+    # headline shape again: calls with different head counts share the scratch
     run_pair(gpu, 40, 8, 128, 32768, 32768, seed=1)
     run_pair(gpu, 14, 2, 64, 513, 1024, seed=2)
+    run_pair(gpu, 32, 32, 128, 4096, 4096, seed=3)
+    run_pair(gpu, 40, 8, 128, 2000, 4096, seed=4)
 
 
 def test_noalloc_argument_checks(fa):
