@@ -244,3 +244,34 @@ def test_merge_forms_share_a_workspace(gpu):
     for it in range(4):
         assert np.array_equal(paged(shared, dl_long, max_seq), ref_long), f"long call {it} on the shared workspace differs"
         assert np.array_equal(paged(shared, dl_short, 256), ref_short), f"short call {it} on the shared workspace differs"
+
+
+def test_paged_long_splits_block_table_fallback(gpu, oracle):
+    """Splits of more than 64 tiles per wave (4480 positions at S = 140000 with 8 kv heads)
+    take the page numbers past the 64th tile from the block table directly instead of from
+    the per-wave page list: bit-identical to the contiguous path and close to the oracle."""
+    fa = gpu
+    Hq, Hkv, d = 8, 8, 128
+    rng = np.random.default_rng(140)
+    kv_dim = Hkv * d
+    lens = [140000, 131200]
+    max_seq = 140000
+    seqs, table, k_pool, v_pool = build_paged(rng, lens, kv_dim, max_seq)
+    q = f16(rng, (len(lens), Hq * d))
+    dq = fa.DeviceBuffer.from_array(q)
+    dk, dv = fa.DeviceBuffer.from_array(k_pool), fa.DeviceBuffer.from_array(v_pool)
+    del k_pool, v_pool
+    dt = fa.DeviceBuffer.from_array(table)
+    dl = fa.DeviceBuffer.from_array(np.array(lens, np.int32))
+    out = fa.DeviceBuffer(q.nbytes)
+    ws = fa.DeviceBuffer(fa.pagedWorkspaceBytes(len(lens), Hq, max_seq))
+    fa.decodeWorkspaceInit(ws)
+    fa.launchPagedDecodeAttention(dq, dk, dv, out, dt, table.shape[1], dl, len(lens), max_seq, Hq, Hkv, d, ws)
+    fa.Hip.sync()
+    got = out.download((len(lens), Hq * d), np.uint16)
+    dk.free()
+    dv.free()
+    for b, S in enumerate(lens):
+        kc, vc = seqs[b]
+        assert np.array_equal(got[b], contiguous_decode(fa, q[b], kc, vc, S, Hq, Hkv, d, max_seq)), f"seq {b} S={S}"
+        assert_close(as_f32(got[b]), oracle.decode(q[b], kc, vc, S, Hq, Hkv, d), f"seq {b} S={S}")
