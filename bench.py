@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the KV-cache path on one MI355X (BASELINE.json metric and configs).
+"""Benchmark of the KV-cache path on one MI355X: the headline metric and the other benchmark configs.
 
 Default (the driver's line): benchmark config 3, the headline. A step is one
 decode token through all 64 layers at Qwen2.5-32B attention shapes (40 query /
@@ -19,9 +19,11 @@ stream the graph runs on. `cpu_baseline` times the reference's own CPU
 attention (cpu_ops.cpp decodeAttention compiled from source into oracle/_ref)
 on this host.
 
---config all additionally prints one JSON line per other benchmark config (BASELINE.json)
+--config all additionally prints one JSON line per other benchmark config
 (1: Qwen2.5-0.5B shapes; 2: 32 layers at 1k/4k/8k, cold and warm; 3 at 16k;
-4: chunked prefill on MFMA with MFMA utilisation; 5: 16 paged sequences).
+4: chunked prefill on MFMA with MFMA utilisation; 5: 16 paged sequences), the int8-KV step,
+the RoPE + KV append rows (T = 1 and 512), and the matmuls either side of attention;
+--config short prints configs 1 and 2 only.
 """
 from __future__ import annotations
 
