@@ -611,7 +611,7 @@ def main():
                          "store per element): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run give the "
                          "counters' reading for a known 1 GiB read + 1 GiB write")
     ap.add_argument("--config", choices=("headline", "all", "others", "short", "prefill", "paged", "q8", "gemm", "layer", "append"), default="headline",
-                    help="headline: the driver's one line; all/others: also (only) the other benchmark configs of BASELINE.json; "
+                    help="headline: the driver's one line; all/others: also (only) the other benchmark configs; "
                          "short: configs 1 and 2 only")
     args = ap.parse_args()
 
