@@ -3,7 +3,7 @@
 Mirrors tests/kernels/test_decode_attention.cu of the reference (Qwen2.5-32B
 shapes 40q/8kv d128, q = 2*N(0,1), seq in {1, 2, 17, 255, 256, 257, 300, 1000,
 2048}, single-pass and split-K with host and device lengths) and adds the
-the benchmark configs of BASELINE.json and the closed-form cases of the softmax rules.
+the benchmark configs and the closed-form cases of the softmax rules.
 """
 import numpy as np
 import pytest
