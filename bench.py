@@ -39,7 +39,7 @@ sys.path.insert(0, os.path.join(ROOT, "friday-inference-engine_amd"))
 
 METRIC = "decode-attn µs/layer-step + KV GB/s (% HBM peak) at 32k ctx, 40q/8kv d128"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 and bf16 MFMA
 MALL_BYTES = 256 << 20         # Infinity Cache: a "cold" working set must exceed it
 
 # HBM traffic of one step-kernel launch at the headline shape: a constant taken from the
@@ -66,10 +66,12 @@ class Ctx:
             raise SystemExit("no HIP device")
         self.bk = C.CDLL(os.path.join(ROOT, "bench_kit", "libfa_benchkit.so"))
         self.bk.fabk_fill_normal_f16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
+        self.bk.fabk_fill_normal_bf16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
         self.stream = fa.Stream()
 
-    def fill(self, buf, n_half, seed, scale=1.0):
-        self.bk.fabk_fill_normal_f16(buf.ptr, n_half, seed, scale, self.stream.s)
+    def fill(self, buf, n_half, seed, scale=1.0, bf16=False):
+        f = self.bk.fabk_fill_normal_bf16 if bf16 else self.bk.fabk_fill_normal_f16
+        f(buf.ptr, n_half, seed, scale, self.stream.s)
 
     def timed(self, fn, steps, warmup, stats=0):
         """Capture fn's launches into a graph; replay warmup + steps times; ms per replay.
@@ -340,9 +342,10 @@ def append_config(cx, T, steps, warmup):
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def prefill_config(cx, p0, steps, warmup, q8=False):
+def prefill_config(cx, p0, steps, warmup, q8=False, bf16=False):
     """benchmark config 4: 512-token causal chunk after p0 cached tokens, 40q/8kv d128, MFMA.
-    q8: int8 caches with one fp16 scale per 32 values (random codes, scales of 0.01 scale)."""
+    q8: int8 caches with one fp16 scale per 32 values (random codes, scales of 0.01 scale).
+    bf16: bf16 q, caches and output on the bf16 MFMA."""
     import numpy as np
 
     fa = cx.fa
@@ -353,25 +356,30 @@ def prefill_config(cx, p0, steps, warmup, q8=False):
     sb = S * Hkv * d // 32 * 2
     L = max(2, -(-2 * MALL_BYTES // (2 * (lb + (sb if q8 else 0)))))  # rotate caches beyond the MALL
     k, v = fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * lb)
-    cx.fill(k, L * lb // 2, 5)  # int8: the fp16 fill's bytes serve as codes
-    cx.fill(v, L * lb // 2, 6)
+    cx.fill(k, L * lb // 2, 5, bf16=bf16)  # int8: the fp16 fill's bytes serve as codes
+    cx.fill(v, L * lb // 2, 6, bf16=bf16)
     ks = vs = None
     if q8:
         ks, vs = fa.DeviceBuffer(L * sb), fa.DeviceBuffer(L * sb)
         cx.fill(ks, L * sb // 2, 8, scale=0.01)
         cx.fill(vs, L * sb // 2, 9, scale=0.01)
     q, out = fa.DeviceBuffer(T * Hq * d * 2), fa.DeviceBuffer(T * Hq * d * 2)
-    cx.fill(q, T * Hq * d, 7)
+    cx.fill(q, T * Hq * d, 7, bf16=bf16)
     pos = fa.DeviceBuffer.from_array(np.array([p0], np.int32))
-    ms = cx.timed(lambda: [fa.launchPrefillAttention(q, k.ptr + l * lb, v.ptr + l * lb, out, T, pos, Hq, Hkv, d,
-                                                     cx.stream.s, k_scale=ks.ptr + l * sb if q8 else None,
-                                                     v_scale=vs.ptr + l * sb if q8 else None)
-                                   for l in range(L)], steps, warmup) / L
+    if bf16:
+        ms = cx.timed(lambda: [fa.launchPrefillAttentionBf16(q, k.ptr + l * lb, v.ptr + l * lb, out, T, pos, Hq, Hkv, d,
+                                                             cx.stream.s) for l in range(L)], steps, warmup) / L
+    else:
+        ms = cx.timed(lambda: [fa.launchPrefillAttention(q, k.ptr + l * lb, v.ptr + l * lb, out, T, pos, Hq, Hkv, d,
+                                                         cx.stream.s, k_scale=ks.ptr + l * sb if q8 else None,
+                                                         v_scale=vs.ptr + l * sb if q8 else None)
+                                       for l in range(L)], steps, warmup) / L
     for b in (k, v, q, out, pos) + ((ks, vs) if q8 else ()):
         b.free()
     flops = 4.0 * d * Hq * (T * p0 + T * (T + 1) / 2)  # causal (unmasked) QK^T and PV flops
     tf = flops / (ms * 1e-3) / 1e12
-    return {"config": "4: chunked prefill" + (" (int8 KV)" if q8 else ""), "T": T, "p0": p0, "heads": f"{Hq}q/{Hkv}kv d{d}",
+    kind = " (int8 KV)" if q8 else (" (bf16)" if bf16 else "")
+    return {"config": "4: chunked prefill" + kind, "T": T, "p0": p0, "heads": f"{Hq}q/{Hkv}kv d{d}",
             "us_per_chunk": round(ms * 1e3, 2), "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
             "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "tokens_per_s": round(T / (ms * 1e-3), 0)}
 
@@ -644,6 +652,8 @@ def main():
             emit(prefill_config(cx, p0, args.steps, args.warmup))
         for p0 in (0, 7680):
             emit(prefill_config(cx, p0, args.steps, args.warmup, q8=True))
+        for p0 in (0, 7680):
+            emit(prefill_config(cx, p0, args.steps, args.warmup, bf16=True))
         emit(paged_config(cx, args.steps, args.warmup))
         for T in (1, 512):
             emit(append_config(cx, T, args.steps, args.warmup))
@@ -666,6 +676,8 @@ def main():
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup)), flush=True)
         for p0 in (0, 2048, 7680):
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup, q8=True)), flush=True)
+        for p0 in (0, 1024, 2048, 4096, 7680):
+            print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup, bf16=True)), flush=True)
     if args.config == "layer":
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True)), flush=True)

@@ -25,6 +25,17 @@ __global__ void fill_normal_f16(_Float16* dst, size_t n, uint32_t seed, float sc
     }
 }
 
+// The same values rounded to bf16 (round to nearest even), stored as raw bits.
+__global__ void fill_normal_bf16(uint16_t* dst, size_t n, uint32_t seed, float scale) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t base = mix32((uint32_t)i * 4u + seed * 0x9e3779b9u);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s += (float)(mix32(base + j) >> 8) * (1.0f / 16777216.0f);
+        dst[i] = __builtin_bit_cast(uint16_t, (__bf16)((s - 2.0f) * 1.7320508f * scale));
+    }
+}
+
 __global__ void copy_u4(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         dst[i] = src[i];
@@ -37,6 +48,12 @@ extern "C" {
 int fabk_fill_normal_f16(void* dst, size_t n, uint32_t seed, float scale, void* stream) {
     hipLaunchKernelGGL(fill_normal_f16, dim3(4096), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<_Float16*>(dst), n, seed, scale);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int fabk_fill_normal_bf16(void* dst, size_t n, uint32_t seed, float scale, void* stream) {
+    hipLaunchKernelGGL(fill_normal_bf16, dim3(4096), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<uint16_t*>(dst), n, seed, scale);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -433,6 +433,20 @@ int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const 
     return launch_status(fa::launch_prefill(p, head_dim, k_scale != nullptr, static_cast<hipStream_t>(stream)), w);
 }
 
+int friday_attn_prefill_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                       uint16_t* out, int T, const int* d_pos0, int num_heads, int num_kv_heads,
+                                       int head_dim, void* stream) {
+    const char* w = "prefill_attention_bf16";
+    if (T <= 0) return ok();
+    if (int rc = check_heads(w, num_heads, num_kv_heads, head_dim)) return rc;
+    if (!q || !k_cache || !v_cache || !out || !d_pos0) return fail(FA_ERR_INVALID, "%s: null argument", w);
+    fa::PrefillParams p{};
+    p.q = q; p.k = k_cache; p.v = v_cache; p.out = out;
+    p.d_pos0 = d_pos0; p.T = T; p.Hq = num_heads; p.Hkv = num_kv_heads; p.G = num_heads / num_kv_heads;
+    p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
+    return launch_status(fa::launch_prefill_bf16(p, head_dim, static_cast<hipStream_t>(stream)), w);
+}
+
 // ---------------- paged ----------------
 
 static int paged_decode_common(const char* w, uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,

@@ -30,6 +30,33 @@ __device__ __forceinline__ f4 mfma16x16x16(h4 a, h4 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// bf16 operands travel in the same 16-bit registers as fp16 ones (h8 holds the raw
+// bits); mma16<true> hands them to the bf16 MFMA (8 bits of significand, fp32 range),
+// mma16<false> to the fp16 one. Both accumulate in fp32.
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+template <bool BF>
+__device__ __forceinline__ f4 mma16(h8 a, h8 b, f4 c) {
+    if constexpr (BF)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// float -> the 16-bit operand type, round to nearest even (bits in a _Float16 slot)
+template <bool BF>
+__device__ __forceinline__ _Float16 to_p(float x) {
+    if constexpr (BF)
+        return __builtin_bit_cast(_Float16, (__bf16)x);
+    else
+        return (_Float16)x;
+}
+
+// eight bf16 ones (0x3F80) in fp16 slots
+__device__ __forceinline__ h8 bf16_splat_one() {
+    const _Float16 one = __builtin_bit_cast(_Float16, (unsigned short)0x3F80);
+    return h8{one, one, one, one, one, one, one, one};
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives in slot k
@@ -70,6 +97,18 @@ __device__ __forceinline__ _Float16 out_half(float r) {
     if (__builtin_isnan(r)) r = 0.0f;
     r = fminf(fmaxf(r, -65504.0f), 65504.0f);
     return (_Float16)r;
+}
+
+// Output element: the fp16 rule above, or for bf16 outputs NaN -> 0 and round to
+// nearest even bf16 (no clamp: bf16 has the fp32 range)
+template <bool BF>
+__device__ __forceinline__ _Float16 out_elem(float r) {
+    if constexpr (BF) {
+        if (__builtin_isnan(r)) r = 0.0f;
+        return __builtin_bit_cast(_Float16, (__bf16)r);
+    } else {
+        return out_half(r);
+    }
 }
 
 __device__ __forceinline__ float wave_max_xor(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }

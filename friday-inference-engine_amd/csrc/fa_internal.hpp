@@ -120,6 +120,8 @@ struct PrefillParams {
 };
 
 int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t stream);
+// bf16 q / K / V / out (fp16 caches only; no counterpart in the reference)
+int launch_prefill_bf16(const PrefillParams& p, int head_dim, hipStream_t stream);
 
 // Prefill projection GEMM (kq_gemm.hip). Weight kinds: the codes of friday_hpc::Q8Kind.
 enum KqKind { kKqQ2K = 1, kKqQ3K = 2, kKqQ4K = 3, kKqQ5K = 4, kKqQ6K = 5, kKqQ80 = 6 };

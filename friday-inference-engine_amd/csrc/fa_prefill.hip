@@ -335,8 +335,9 @@ struct P2Lds {
     static constexpr int B2 = Q8 ? RAWB : 16;
 };
 
-template <int D, int RA, int RB, bool Q8>
+template <int D, int RA, int RB, bool Q8, bool BF>
 __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParams p) {
+    static_assert(!(Q8 && BF), "int8 caches decode to fp16");
     using Gm = P2Geo<D>;
     using Rg = P2RawGeo<D>;
     using Lb = P2Lds<D, Q8>;
@@ -503,7 +504,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
         for (int i = 0; i < Gm::DTILES; ++i) o[rt][i] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
+    const h8 ones = BF ? bf16_splat_one() : h8{1, 1, 1, 1, 1, 1, 1, 1};
     const int wrow = sl * kP2KW;  // first stage row of this wave's keys
 
     // one stage's work for the group's N row tiles: S^T = K Q^T, online softmax, O^T += V^T P^T
@@ -528,7 +529,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                 for (int mt = 0; mt < 2; ++mt) {
                     sacc[rt][mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int s = 0; s < Gm::KSTEPS; ++s) sacc[rt][mt] = mfma16x16x32(ka[mt][s], qf[rt][s], sacc[rt][mt]);
+                    for (int s = 0; s < Gm::KSTEPS; ++s) sacc[rt][mt] = mma16<BF>(ka[mt][s], qf[rt][s], sacc[rt][mt]);
                 }
             // phase 2: online softmax in the log2 domain; lane column = row, k-slots = keys.
             // x = raw score (its scale, scale * log2(e), is applied in the max and the weight
@@ -583,7 +584,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                 const float nb = kNegBig - m_run[rt];
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    pf[rt][j] = (_Float16)exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), nb));
+                    pf[rt][j] = to_p<BF>(exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), nb)));
             }
             if (!full) {
 #pragma unroll
@@ -612,8 +613,8 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 #pragma unroll
             for (int rt = 0; rt < N; ++rt) {
 #pragma unroll
-                for (int dt = 0; dt < Gm::DTILES; ++dt) o[rt][dt] = mfma16x16x32(va[dt], pf[rt], o[rt][dt]);
-                ol[rt] = mfma16x16x32(ones, pf[rt], ol[rt]);
+                for (int dt = 0; dt < Gm::DTILES; ++dt) o[rt][dt] = mma16<BF>(va[dt], pf[rt], o[rt][dt]);
+                ol[rt] = mma16<BF>(ones, pf[rt], ol[rt]);
             }
         }
     };
@@ -698,7 +699,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                 const int t = r / p.G, g = r % p.G;
                 h4 v;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
+                for (int i = 0; i < 4; ++i) v[i] = out_elem<BF>(L > 1e-12f ? O[i] / L : 0.0f);
                 *reinterpret_cast<h4*>(reinterpret_cast<_Float16*>(p.out) + (size_t)t * qd + (size_t)(kvh * p.G + g) * D + 4 * d4) = v;
             }
         }
@@ -706,12 +707,12 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     }
 }
 
-template <int D, int RA, int RB, bool Q8>
+template <int D, int RA, int RB, bool Q8, bool BF>
 int launch_dma(const PrefillParams& p, hipStream_t stream) {
     const int R = p.T * p.G;
     constexpr int rows = (RA + RB) * 16;
     const dim3 grid(p.Hkv, (R + rows - 1) / rows);
-    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RA, RB, Q8>), grid, dim3(kP2Threads), 0, stream, p);
+    hipLaunchKernelGGL((fa_prefill_dma_kernel<D, RA, RB, Q8, BF>), grid, dim3(kP2Threads), 0, stream, p);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -719,7 +720,7 @@ int launch_dma(const PrefillParams& p, hipStream_t stream) {
 // whole launch; group 0 takes ceil(RT/2) of them, group 1 the rest, at most three per
 // wave so that the registers of two waves per SIMD hold them (RT 1..6: (1,0), (1,1),
 // (2,1), (2,2), (3,2), (3,3)).
-template <int D, bool Q8>
+template <int D, bool Q8, bool BF = false>
 int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     static const int forced = [] {
         const char* e = std::getenv("FRIDAY_ATTN_PREFILL_RT");
@@ -730,12 +731,12 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     const int rt_max = 6;
     rt = rt < 1 ? 1 : (rt > rt_max ? rt_max : rt);
     switch (rt) {
-        case 1: return launch_dma<D, 1, 0, Q8>(p, stream);
-        case 2: return launch_dma<D, 1, 1, Q8>(p, stream);
-        case 3: return launch_dma<D, 2, 1, Q8>(p, stream);
-        case 4: return launch_dma<D, 2, 2, Q8>(p, stream);
-        case 5: return launch_dma<D, 3, 2, Q8>(p, stream);
-        default: return launch_dma<D, 3, 3, Q8>(p, stream);
+        case 1: return launch_dma<D, 1, 0, Q8, BF>(p, stream);
+        case 2: return launch_dma<D, 1, 1, Q8, BF>(p, stream);
+        case 3: return launch_dma<D, 2, 1, Q8, BF>(p, stream);
+        case 4: return launch_dma<D, 2, 2, Q8, BF>(p, stream);
+        case 5: return launch_dma<D, 3, 2, Q8, BF>(p, stream);
+        default: return launch_dma<D, 3, 3, Q8, BF>(p, stream);
     }
 }
 
@@ -759,6 +760,12 @@ int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t st
     if (head_dim == 64)
         return !q8 ? launch_dma_rt<64, false>(p, stream)
                    : scale_dma ? launch_dma_rt<64, true>(p, stream) : launch_pf<64, true>(p, stream);
+    return -2;
+}
+
+int launch_prefill_bf16(const PrefillParams& p, int head_dim, hipStream_t stream) {
+    if (head_dim == 128) return launch_dma_rt<128, false, true>(p, stream);
+    if (head_dim == 64) return launch_dma_rt<64, false, true>(p, stream);
     return -2;
 }
 

@@ -51,6 +51,7 @@ API = [
      [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_prefill_supported", _I, [_I, _I, _I]),
     ("friday_attn_prefill_attention", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    ("friday_attn_prefill_attention_bf16", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
     ("friday_attn_paged_workspace_bytes", _SZ, [_I, _I, _I]),
     ("friday_attn_paged_rope_store_kv", _I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
     ("friday_attn_paged_decode_step", _I,
@@ -372,6 +373,12 @@ def launchPrefillAttention(q, k_cache, v_cache, out, T, d_pos0, num_heads, num_k
     _check(load().friday_attn_prefill_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), T, _ptr(d_pos0),
                                                 num_heads, num_kv_heads, head_dim, stream, _ptr(k_scale),
                                                 _ptr(v_scale)))
+
+
+def launchPrefillAttentionBf16(q, k_cache, v_cache, out, T, d_pos0, num_heads, num_kv_heads, head_dim, stream=None):
+    """launchPrefillAttention with bf16 q / K / V / out (no counterpart in the reference)."""
+    _check(load().friday_attn_prefill_attention_bf16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), T,
+                                                     _ptr(d_pos0), num_heads, num_kv_heads, head_dim, stream))
 
 
 def pagedWorkspaceBytes(batch, num_heads, max_seq_len) -> int:

@@ -187,6 +187,14 @@ int friday_attn_prefill_supported(int num_heads, int num_kv_heads, int head_dim)
 int friday_attn_prefill_attention(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out, int T,
                                   const int* d_pos0, int num_heads, int num_kv_heads, int head_dim, void* stream,
                                   const uint16_t* k_scale, const uint16_t* v_scale);
+/* The same causal prefill with bf16 q, K/V cache and out (bf16 MFMA operands, fp32
+ * scores and softmax, weights rounded to bf16 for the PV product, output NaN -> 0 and
+ * round to nearest even bf16). No counterpart in the reference, whose caches are fp16
+ * (attention_kernels.cu:513-645); it serves callers that keep bf16 activations and
+ * caches, the input type the prefill benchmark allows besides fp16. */
+int friday_attn_prefill_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                       uint16_t* out, int T, const int* d_pos0, int num_heads, int num_kv_heads,
+                                       int head_dim, void* stream);
 
 /* ---------------- paged multi-sequence decode ----------------
  * Semantics of the (unbuilt) experimental paged cache: 16-token pages, physical

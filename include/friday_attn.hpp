@@ -84,6 +84,19 @@ inline void launchPrefillAttention(const void* q, const void* k_cache, const voi
                                                 num_heads, num_kv_heads, head_dim, stream, detail::h(k_scale),
                                                 detail::h(v_scale)));
 }
+// bf16 q / caches / out (friday_attn_prefill_attention_bf16; no reference counterpart)
+inline void launchPrefillAttentionBf16(const void* q, const void* k_cache, const void* v_cache, void* out, int T,
+                                       const int* d_pos0, int num_heads, int num_kv_heads, int head_dim,
+                                       hipStream_t stream) {
+    if (T <= 0) return;
+    if (!prefillAttentionSupported(num_heads, num_kv_heads, head_dim)) {
+        std::fprintf(stderr, "launchPrefillAttentionBf16: unsupported head layout\n");
+        std::abort();
+    }
+    detail::check(friday_attn_prefill_attention_bf16(detail::h(q), detail::h(k_cache), detail::h(v_cache),
+                                                     detail::h(out), T, d_pos0, num_heads, num_kv_heads, head_dim,
+                                                     stream));
+}
 
 // ---- the kernels transformer.cpp launches directly
 // ropeStoreKvKernel (cuda_math_kernels.cu:363-404; T tokens = grid.y there); the rope

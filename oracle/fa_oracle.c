@@ -20,7 +20,10 @@
  *   prefill        row t equals decode at S = p0+t+1 by construction, causal
  *                  perturbation invariance;
  *   q8 append      closed forms (zero block, amax element maps to +-127,
- *                  dequant error <= dh/2) and brute-force rne.
+ *                  dequant error <= dh/2) and brute-force rne;
+ *   bf16 prefill   (no reference counterpart) conversions vs torch bfloat16,
+ *                  exhaustive / 200k patterns; equals the fp16 prefill up to the
+ *                  final rounding on inputs both types hold; fp64 brute force.
  */
 #include "fa_oracle.h"
 
@@ -95,6 +98,30 @@ void or_halves_to_floats(const uint16_t* h, float* f, size_t n) {
 
 void or_floats_to_halves(const float* f, uint16_t* h, size_t n) {
     for (size_t i = 0; i < n; ++i) h[i] = or_float_to_half(f[i]);
+}
+
+/* ---- bf16 (no reference counterpart: the reference caches are fp16). The top 16
+ * bits of an fp32; float -> bf16 rounds to nearest even on the dropped 16 bits. ---- */
+
+float or_bf16_to_float(uint16_t b) {
+    const uint32_t x = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+uint16_t or_float_to_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u); /* NaN stays NaN (quiet) */
+    const uint32_t lsb = (x >> 16) & 1u;
+    return (uint16_t)((x + 0x7fffu + lsb) >> 16);
+}
+
+/* output rule of the bf16 prefill: NaN -> 0, round to nearest even bf16 */
+float or_round_to_bf16(float v) {
+    if (isnan(v)) v = 0.0f;
+    return or_bf16_to_float(or_float_to_bf16(v));
 }
 
 /* ---- RoPE (cpu_ops.cpp:26-43) ---- */
@@ -186,9 +213,15 @@ static float get_f16(const void* cache, const uint16_t* scale, size_t idx) {
 static float get_q8(const void* cache, const uint16_t* scale, size_t idx) {
     return (float)((const int8_t*)cache)[idx] * or_half_to_float(scale[idx / 32]);
 }
+static float get_bf16(const void* cache, const uint16_t* scale, size_t idx) {
+    (void)scale;
+    return or_bf16_to_float(((const uint16_t*)cache)[idx]);
+}
 
-static void decode_generic(const uint16_t* q, const void* kc, const uint16_t* ks, const void* vc, const uint16_t* vs,
-                           kv_get_fn get, float* out, int S, int Hq, int Hkv, int hd, int kv_stride) {
+/* bf16 != 0: q, K, V are bf16 and the output takes the bf16 rule (or_round_to_bf16);
+ * otherwise fp16 q and the reference's fp16 output rule (or_round_to_half) */
+static void decode_any(const uint16_t* q, const void* kc, const uint16_t* ks, const void* vc, const uint16_t* vs,
+                       kv_get_fn get, float* out, int S, int Hq, int Hkv, int hd, int kv_stride, int bf16) {
     const int per_kv = Hq / Hkv;
     const float scale = 1.0f / sqrtf((float)hd);
     float* s = (float*)malloc(sizeof(float) * (S > 0 ? S : 1));
@@ -196,7 +229,7 @@ static void decode_generic(const uint16_t* q, const void* kc, const uint16_t* ks
     float* qf = (float*)malloc(sizeof(float) * hd);
     for (int h = 0; h < Hq; ++h) {
         const int kvh = h / per_kv;
-        for (int d = 0; d < hd; ++d) qf[d] = or_half_to_float(q[h * hd + d]);
+        for (int d = 0; d < hd; ++d) qf[d] = bf16 ? or_bf16_to_float(q[h * hd + d]) : or_half_to_float(q[h * hd + d]);
         float mx = -1e30f;
         for (int p = 0; p < S; ++p) {
             const size_t base = (size_t)p * kv_stride + (size_t)kvh * hd;
@@ -220,11 +253,16 @@ static void decode_generic(const uint16_t* q, const void* kc, const uint16_t* ks
             const size_t base = (size_t)p * kv_stride + (size_t)kvh * hd;
             for (int d = 0; d < hd; ++d) acc[d] += w * get(vc, vs, base + d);
         }
-        for (int d = 0; d < hd; ++d) out[h * hd + d] = or_round_to_half(acc[d]);
+        for (int d = 0; d < hd; ++d) out[h * hd + d] = bf16 ? or_round_to_bf16(acc[d]) : or_round_to_half(acc[d]);
     }
     free(s);
     free(acc);
     free(qf);
+}
+
+static void decode_generic(const uint16_t* q, const void* kc, const uint16_t* ks, const void* vc, const uint16_t* vs,
+                           kv_get_fn get, float* out, int S, int Hq, int Hkv, int hd, int kv_stride) {
+    decode_any(q, kc, ks, vc, vs, get, out, S, Hq, Hkv, hd, kv_stride, 0);
 }
 
 void or_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int S,
@@ -350,6 +388,16 @@ void or_prefill_attention_q8(const uint16_t* q, const int8_t* k_cache, const uin
     const size_t qd = (size_t)Hq * hd;
     for (int t = 0; t < T; ++t)
         or_decode_attention_q8(q + t * qd, k_cache, k_scale, v_cache, v_scale, out + t * qd, p0 + t + 1, Hq, Hkv, hd);
+}
+
+/* bf16 q / caches / output: the same causal rows in the same order, bf16 inputs
+ * widened exactly, the output rounded by or_round_to_bf16 */
+void or_prefill_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int T,
+                               int p0, int Hq, int Hkv, int hd) {
+    const size_t qd = (size_t)Hq * hd;
+    for (int t = 0; t < T; ++t)
+        decode_any(q + t * qd, k_cache, NULL, v_cache, NULL, get_bf16, out + t * qd, p0 + t + 1, Hq, Hkv, hd,
+                   Hkv * hd, 1);
 }
 
 /* ---- paged addressing (paged_attention.cu:29-41: phys = table[pos/16], row pos%16) ---- */

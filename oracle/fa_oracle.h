@@ -12,6 +12,8 @@
  *   - split-K partials + LSE merge attention_kernels.cu:131-235, 267-411
  *   - causal prefill attention     attention_kernels.h:36-45 (row t == decode at p0+t+1)
  *   - paged addressing             experimental/runtime/src/kernels/paged_attention.cu:18-45
+ *   - bf16 prefill (no counterpart: the reference caches are fp16): the causal prefill
+ *     above with bf16 inputs widened exactly and the output rounded to bf16
  *
  * fp16 values travel as uint16_t bit patterns. Every accumulation is fp32 in
  * the reference's order unless a function name says f64.
@@ -31,6 +33,10 @@ float or_half_to_float(uint16_t h);
 uint16_t or_float_to_half(float f);
 /* NaN -> 0, clamp to +-65504, then RNE to fp16 precision (returned as float). */
 float or_round_to_half(float x);
+/* bf16 <-> fp32 (round to nearest even); or_round_to_bf16: NaN -> 0, then rounded */
+float or_bf16_to_float(uint16_t b);
+uint16_t or_float_to_bf16(float f);
+float or_round_to_bf16(float x);
 void or_halves_to_floats(const uint16_t* h, float* f, size_t n);
 void or_floats_to_halves(const float* f, uint16_t* h, size_t n);
 
@@ -72,6 +78,9 @@ void or_prefill_attention(const uint16_t* q, const uint16_t* k_cache, const uint
                           int p0, int Hq, int Hkv, int head_dim);
 void or_prefill_attention_q8(const uint16_t* q, const int8_t* k_cache, const uint16_t* k_scale, const int8_t* v_cache,
                              const uint16_t* v_scale, float* out, int T, int p0, int Hq, int Hkv, int head_dim);
+/* or_prefill_attention with bf16 q / caches and the bf16 output rule (no reference counterpart) */
+void or_prefill_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int T,
+                               int p0, int Hq, int Hkv, int hd);
 
 /* Paged layout: pool [num_pages][page][kv_dim]; block_table row of one sequence.
  * Gathers positions [0, S) into a contiguous [S][kv_dim] buffer. */

@@ -58,6 +58,13 @@ class Oracle:
         L.or_decode_attention_split.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_lse_merge.argtypes = [_f32p, _f32p, _f32p, _i, _i, _f32p]
         L.or_prefill_attention.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
+        L.or_bf16_to_float.restype = C.c_float
+        L.or_bf16_to_float.argtypes = [C.c_uint16]
+        L.or_float_to_bf16.restype = C.c_uint16
+        L.or_float_to_bf16.argtypes = [C.c_float]
+        L.or_round_to_bf16.restype = C.c_float
+        L.or_round_to_bf16.argtypes = [C.c_float]
+        L.or_prefill_attention_bf16.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_prefill_attention_q8.argtypes = [_u16p, _i8p, _u16p, _i8p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_paged_gather.argtypes = [_u16p, _i32p, _i, _i, _i, _u16p]
         L.or_q8_row_bytes.restype = C.c_size_t
@@ -142,6 +149,13 @@ class Oracle:
         out = np.empty((T, Hq * d), np.float32)
         self.lib.or_prefill_attention(_f16bits(q).ravel(), _f16bits(kc).ravel(), _f16bits(vc).ravel(), out.ravel(),
                                       T, p0, Hq, Hkv, d)
+        return out
+
+    def prefill_bf16(self, q, kc, vc, T, p0, Hq, Hkv, d) -> np.ndarray:
+        """q / kc / vc: bf16 bit patterns (uint16 arrays)."""
+        out = np.empty((T, Hq * d), np.float32)
+        u16 = lambda a: np.ascontiguousarray(a, np.uint16).ravel()
+        self.lib.or_prefill_attention_bf16(u16(q), u16(kc), u16(vc), out.ravel(), T, p0, Hq, Hkv, d)
         return out
 
     def prefill_q8(self, q, k8, ks, v8, vs, T, p0, Hq, Hkv, d) -> np.ndarray:

@@ -14,6 +14,16 @@ def f16(rng, shape, scale=1.0):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(np.float16).view(np.uint16)
 
 
+def bf16(rng, shape, scale=1.0):
+    """N(0, scale^2) rounded to nearest even bf16, returned as uint16 bits."""
+    x = (rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)).view(np.uint32)
+    return ((x + np.uint32(0x7FFF) + ((x >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
+
+
+def bf16_as_f32(bits):
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
 def as_f32(bits):
     return np.asarray(bits).view(np.float16).astype(np.float32)
 

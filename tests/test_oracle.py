@@ -5,7 +5,8 @@ Every oracle function is checked against something it does not restate:
     (tests/golden/make_golden.py: friday_cpu::rope / decodeAttention compiled
     from cpu_ops.cpp), bit for bit;
   * the live reference build in oracle/_ref when present (build container);
-  * numpy's IEEE fp16 conversion, exhaustively;
+  * numpy's IEEE fp16 conversion and torch's bf16 conversion, exhaustively or
+    on large samples;
   * float64 brute force and closed forms of the softmax rules.
 """
 import os
@@ -13,7 +14,7 @@ import os
 import numpy as np
 import pytest
 
-from fa_helpers import f16
+from fa_helpers import bf16, bf16_as_f32, f16
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLDEN = os.path.join(HERE, "golden", "golden_cpu_path.npz")
@@ -199,6 +200,92 @@ def test_prefill_is_causal_decode(oracle):
     kc2[p0 + 5:] = f16(rng, kc2[p0 + 5:].shape, 9.0)
     out2 = oracle.prefill(q, kc2, vc, T, p0, Hq, Hkv, d)
     assert np.array_equal(out[:5], out2[:5])
+
+
+# ---------------------------------------------------------------- bf16 rules
+def test_bf16_to_float_exhaustive(oracle):
+    import torch
+    bits = np.arange(65536, dtype=np.uint16)
+    got = np.array([oracle.lib.or_bf16_to_float(int(b)) for b in bits], np.float32)
+    exp = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    same = (got.view(np.uint32) == exp.view(np.uint32)) | (np.isnan(got) & np.isnan(exp))
+    assert same.all()
+
+
+def test_float_to_bf16_rne(oracle):
+    """torch's float -> bfloat16 (round to nearest even) on random bit patterns, ties,
+    the neighbours of ties, subnormals, infinities and NaN."""
+    import torch
+    rng = np.random.default_rng(41)
+    x = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    base = rng.integers(0, 2**16, 2000, dtype=np.uint64).astype(np.uint32) << 16
+    ties = np.concatenate([base | 0x8000, base | 0x7FFF, base | 0x8001, base | 0x10000 | 0x8000])
+    edges = np.array([0, 0x80000000, 1, 0x007FFFFF, 0x7F7FFFFF, 0x7F7F8000, 0x7F800000, 0xFF800000, 0x7FC00000,
+                      0x7F800001, 0x3F808000, 0x3F818000], np.uint32)
+    bits = np.concatenate([x, ties.astype(np.uint32), edges])
+    f = bits.view(np.float32)
+    got = np.array([oracle.lib.or_float_to_bf16(float(v)) for v in f], np.uint16)
+    exp = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(f)
+    assert np.array_equal(got[~nan], exp[~nan])
+    assert np.isnan(bf16_as_f32(got[nan])).all()
+    assert oracle.lib.or_round_to_bf16(float("nan")) == 0.0
+
+
+def _bf16_bits_exact(x):
+    """bf16 bits of float32 values that bf16 holds exactly (the low 16 bits are zero)."""
+    b = np.asarray(x, np.float32).view(np.uint32)
+    assert not (b & 0xFFFF).any()
+    return (b >> 16).astype(np.uint16)
+
+
+def _dual_values(rng, shape):
+    """Values exact in fp16 and in bf16 (m * 2^-6, |m| < 256): fp16 bits, bf16 bits."""
+    m = rng.integers(-255, 256, shape).astype(np.float32) * np.float32(2.0**-6)
+    return m.astype(np.float16).view(np.uint16), _bf16_bits_exact(m)
+
+
+def test_prefill_bf16_matches_fp16_path_on_shared_values(oracle):
+    """On inputs that fp16 and bf16 both hold exactly, the two prefills accumulate the same
+    fp32 values in the same order: they differ only in the final rounding. So the bf16
+    output is the bf16 rounding of the fp16 output wherever that fp16 value is not a
+    bf16 midpoint (double rounding fp32 -> fp16 -> bf16 only differs there). A transposed
+    operand, a wrong cache or head index, or a wrong widening would break this."""
+    rng = np.random.default_rng(42)
+    Hq, Hkv, d, T, p0 = 12, 4, 64, 7, 30
+    q16, qb = _dual_values(rng, (T, Hq * d))
+    k16, kb = _dual_values(rng, (p0 + T, Hkv * d))
+    v16, vb = _dual_values(rng, (p0 + T, Hkv * d))
+    o16 = oracle.prefill(q16, k16, v16, T, p0, Hq, Hkv, d)
+    ob = oracle.prefill_bf16(qb, kb, vb, T, p0, Hq, Hkv, d)
+    rounded = np.array([oracle.lib.or_round_to_bf16(float(v)) for v in o16.ravel()], np.float32).reshape(o16.shape)
+    # fp16 outputs that sit exactly halfway between two bf16 values: there the fp32 value
+    # may lie on either side, so the bf16 output is either neighbour
+    tie = (o16.view(np.uint32) & 0xFFFF) == 0x8000
+    assert np.array_equal(rounded[~tie], ob[~tie])
+    lo = (o16.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    hi = ((o16.view(np.uint32) & 0xFFFF0000) + 0x10000).view(np.float32)
+    assert ((ob[tie] == lo[tie]) | (ob[tie] == hi[tie])).all()
+    _bf16_bits_exact(ob)  # every output is a bf16 value
+
+
+def test_prefill_bf16_f64_brute_force(oracle):
+    """Against float64 attention over the widened bf16 inputs: the oracle's only errors
+    are fp32 accumulation and the final bf16 rounding (half a bf16 step, 2^-9 relative)."""
+    rng = np.random.default_rng(43)
+    Hq, Hkv, d, T, p0 = 8, 2, 128, 5, 60
+    q, k, v = bf16(rng, (T, Hq * d)), bf16(rng, (p0 + T, Hkv * d)), bf16(rng, (p0 + T, Hkv * d))
+    got = oracle.prefill_bf16(q, k, v, T, p0, Hq, Hkv, d)
+    qf, kf, vf = (bf16_as_f32(a).astype(np.float64) for a in (q, k, v))
+    G = Hq // Hkv
+    for t in range(T):
+        S = p0 + t + 1
+        for hh in range(Hq):
+            kv = hh // G
+            s = kf[:S, kv * d:(kv + 1) * d] @ qf[t, hh * d:(hh + 1) * d] / np.sqrt(d)
+            w = np.exp(s - s.max())
+            ref = (w / w.sum()) @ vf[:S, kv * d:(kv + 1) * d]
+            np.testing.assert_allclose(got[t, hh * d:(hh + 1) * d], ref, rtol=2.0**-8, atol=1e-5)
 
 
 def test_store_kv_q8_rules(oracle):
