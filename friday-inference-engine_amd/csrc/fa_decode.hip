@@ -25,12 +25,18 @@
 namespace fa {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // waves per workgroup (the merge kernel, fp16 and paged decode)
 constexpr int kThreads = kWaves * 64;
 constexpr int kTile = 16;  // positions per wave tile
 constexpr int kStages = 1;    // register stages (tiles in flight) per wave
-// int8 rows are half as wide: twice the tiles in flight keep the same bytes in flight
-constexpr int kStagesQ8 = 2;
+// Contiguous int8 caches: the loop issues about 2.4x the instructions of the fp16 one per
+// tile (the dequantisation), and with one wave per SIMD issue time and memory waits add up.
+// Eight waves of one tile in flight each (the fp16 bytes in flight per CU, two waves per
+// SIMD, one workgroup per CU) let one wave's issue overlap the other's wait.
+constexpr int kWavesQ8 = 8;
+constexpr int kStagesQ8 = 1;
+// waves per workgroup of a decode kernel
+constexpr int waves_for(bool paged, bool q8) { return q8 && !paged ? kWavesQ8 : kWaves; }
 constexpr int kShortStages = 4;  // stages when a wave has at most this many tiles
 // Paged grids hold several workgroups per CU: three per CU (at most 168 registers), and at
 // most two tiles in flight per wave in the short-split form, where four made the waves of a
@@ -44,7 +50,7 @@ constexpr float kLazy2 = 8.0f;   // lazy softmax reference: rescale when a max r
 // ALIAS: the wave combine reuses the tile region (after a barrier), so that two workgroups
 // fit in a CU's LDS with room to spare; used by the paged kernel, whose grids hold many
 // workgroups per CU. Otherwise the combine has a region of its own and needs no barrier.
-template <int D, bool Q8, bool ALIAS>
+template <int D, bool Q8, bool ALIAS, int W>
 struct Geo {
     static constexpr int LROW = D * 2 + 16;           // LDS row stride in bytes (fp16 row + 16 B pad)
     static constexpr int KSTEPS = D / 32;             // MFMA k-steps over the head dimension
@@ -56,8 +62,8 @@ struct Geo {
     static constexpr int NLD = kTile / RPI;           // loads per tile per tensor
     static constexpr int WAVE_LDS = 2 * kTile * LROW;  // K and V tile of one wave
     static constexpr int CROW = D + 4;                 // combine row stride in floats (bank spread)
-    static constexpr int COMB_LDS = (2 * kWaves * 16 + kWaves * 16 * CROW) * 4;
-    static constexpr int TILES = kWaves * WAVE_LDS;
+    static constexpr int COMB_LDS = (2 * W * 16 + W * 16 * CROW) * 4;
+    static constexpr int TILES = W * WAVE_LDS;
     static constexpr int COMB_OFF = ALIAS ? 0 : TILES;
     static constexpr int QX_OFF = ALIAS ? (TILES > COMB_LDS ? TILES : COMB_LDS) : TILES + COMB_LDS;  // rotated q rows
     static constexpr int LDS = QX_OFF + 16 * D * 2;  // tiles, the wave combine, the q rows (16 heads x D fp16)
@@ -177,9 +183,9 @@ __device__ __forceinline__ float max8(float v) {
 // does not depend on the column range or on which workgroup runs it, so the separate
 // merge kernel and the column slices of the fused merge give the same bits. cw must be a
 // power of two; with out_q, cw and c0 must be multiples of 8.
-template <int D>
+template <int D, int NT>  // NT: threads of the workgroup
 __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, int c0, int cw) {
-    constexpr int kUnitsPerPass = kThreads / 8;
+    constexpr int kUnitsPerPass = NT / 8;
     constexpr int kBatch = 4;  // passes whose partials are loaded in one round trip
     const int tid = threadIdx.x, r = tid & 7;
     const int wunit = __builtin_amdgcn_readfirstlane(tid >> 6) * 8;  // first unit of this wave in a pass
@@ -249,16 +255,16 @@ __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, 
 }
 
 // Whole-row merge of nh head rows.
-template <int D>
+template <int D, int NT>
 __device__ __forceinline__ void merge_any(const DecodeParams& p, size_t row0, int nh, int nsp) {
-    merge_cols<D>(p, row0, nh, nsp, 0, D / 4);
+    merge_cols<D, NT>(p, row0, nh, nsp, 0, D / 4);
 }
 
 // Column slice k of nslice of the fused merge.
-template <int D>
+template <int D, int NT>
 __device__ __forceinline__ void merge_slice(const DecodeParams& p, size_t row0, int nh, int nsp, int k, int nslice) {
     const int cw = (D / 4) / nslice;
-    merge_cols<D>(p, row0, nh, nsp, k * cw, cw);
+    merge_cols<D, NT>(p, row0, nh, nsp, k * cw, cw);
 }
 
 // Number of column slices the fused merge of a group is spread over: the launcher's
@@ -284,10 +290,15 @@ __device__ __forceinline__ void wait_count(const unsigned* cnt, unsigned target)
     }
 }
 
+// Workgroups per CU the register budget is set for: fp16 two (two waves per SIMD, up to 256
+// registers), paged three (up to 168), contiguous int8 one of eight waves (two per SIMD).
+constexpr int wgs_per_cu(bool paged, bool q8) { return paged ? kPagedWgsPerCu : (q8 ? 1 : 2); }
+
 template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
-// two workgroups per CU (two waves per SIMD) must fit: a 256-register budget; paged: three
-__global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decode_kernel(DecodeParams p) {
-    using Gm = Geo<D, Q8, PAGED>;
+__global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) void fa_decode_kernel(DecodeParams p) {
+    constexpr int W = waves_for(PAGED, Q8);  // waves of this workgroup
+    constexpr int NT = W * 64;
+    using Gm = Geo<D, Q8, PAGED, W>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
 
     // grid x = (kv head, head block) group, y = split: consecutive workgroup ids walk the
@@ -355,7 +366,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     // S-1. They are issued before the first K/V tile and used after it is in flight. A
     // chunk is the 16 bytes one lane moves per cache row: 8 fp16 values, or 16 int8 ones.
     constexpr int HD2 = D / 2;
-    constexpr int TPH = kThreads / 16;            // threads per head column in the q rotation
+    constexpr int TPH = NT / 16;                  // threads per head column in the q rotation
     constexpr int PPT = ROPE ? HD2 / TPH : 1;     // q rotation pairs per thread (16 head columns x D/2 pairs)
     constexpr int CW = Q8 ? 16 : 8;                       // values of one row chunk
     constexpr int NH = ROPE ? CW / 8 : 1;                 // fp16 vectors of one row chunk
@@ -374,7 +385,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         rot_q = S > 0 && S_raw == S;
         if (rot_q && split == nsp - 1) {
             const int last_tile = (end - start - 1) / kTile;
-            append_wave = last_tile % kWaves;
+            append_wave = last_tile % W;
             append_tile = last_tile;
             append_row = (S - 1) - (start + last_tile * kTile);
         }
@@ -535,7 +546,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     static_assert(kTile == kPageTokens, "one page per tile");
     int wpages = 0;
     if constexpr (PAGED) {
-        const int pt = start + (wave + kWaves * lane) * kTile;
+        const int pt = start + (wave + W * lane) * kTile;
         wpages = pt < end ? p.block_table[(size_t)b * p.bt_stride + (pt >> 4)] : 0;
     }
     const uint32_t lane_off = (uint32_t)(lrow * rowb + lchunk * 16);
@@ -546,7 +557,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         const uint32_t nrows = (uint32_t)min(max(end - base, 0), kTile);
         size_t row0 = (size_t)base;  // cache row of the tile's first position
         if constexpr (PAGED) {
-            const int li = (t - wave) / kWaves;  // this wave's tile number (uniform)
+            const int li = (t - wave) / W;  // this wave's tile number (uniform)
             int phys;
             if (li < 64)
                 phys = __builtin_amdgcn_readlane(wpages, li);
@@ -588,8 +599,10 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
                 cv[r] = copy_here(st.v[r]);
                 sk[r] = f16_bits_here(st.ks[r]);
                 sv[r] = f16_bits_here(st.vs[r]);
+                // the new row, as quantized and written to the cache by this wave (selects on
+                // the raw codes: cheaper here than rewriting the dequantised row afterwards)
                 if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
-                    ck[r] = kq;  // the new row, as quantized and written to the cache by this wave
+                    ck[r] = kq;
                     cv[r] = vq;
                     sk[r] = (_Float16)ksc;  // fp16 values: exact
                     sv[r] = (_Float16)vsc;
@@ -614,13 +627,16 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
 #pragma unroll
             for (int r = 0; r < Gm::NLD; ++r) {
                 const int row = r * Gm::RPI + lrow;
-                u4 kx = st.k[r], vx = st.v[r];
-                if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
-                    kx = rk;  // the new row, as written to the cache by this wave
-                    vx = *reinterpret_cast<const u4*>(&nv[0]);
+                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = st.k[r];
+                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = st.v[r];
+            }
+            // the new row, as written to the cache by this wave, over the one just loaded (a
+            // wave's LDS writes complete in order); one tile of one wave
+            if (ROPE && t == append_tile && wave == append_wave) {
+                if (lrow == append_row % Gm::RPI) {
+                    *reinterpret_cast<u4*>(kl + append_row * Gm::LROW + lchunk * 16) = rk;
+                    *reinterpret_cast<u4*>(vl + append_row * Gm::LROW + lchunk * 16) = *reinterpret_cast<const u4*>(&nv[0]);
                 }
-                *reinterpret_cast<u4*>(kl + row * Gm::LROW + lchunk * 16) = kx;
-                *reinterpret_cast<u4*>(vl + row * Gm::LROW + lchunk * 16) = vx;
             }
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
@@ -682,30 +698,30 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         __builtin_amdgcn_wave_barrier();
     };
 
-    // uniform trip count: groups of N tiles of this wave (tiles wave, wave + kWaves, ...).
+    // uniform trip count: groups of N tiles of this wave (tiles wave, wave + W, ...).
     // Long splits keep one tile in flight per wave (more congests HBM); short ones, whose
     // waves have at most four tiles, issue them all at once (one memory latency).
-    const int my_tiles = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+    const int my_tiles = ntiles > wave ? (ntiles - wave + W - 1) / W : 0;
     auto stream = [&](auto n_tag) {
         constexpr int N = decltype(n_tag)::value;
         Stage st[N];
         const int groups = (my_tiles + N - 1) / N;
         if (groups > 0) {
 #pragma unroll
-            for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * kWaves);
+            for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * W);
         }
         load_inputs();
         prepare();
         for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
             for (int s = 0; s < N; ++s) {
-                const int ts = wave + (gi * N + s) * kWaves;
-                consume(st[s], ts, ts + N * kWaves);
+                const int ts = wave + (gi * N + s) * W;
+                consume(st[s], ts, ts + N * W);
             }
         }
     };
     constexpr int kShort = PAGED ? kShortStagesPaged : kShortStages;
-    if ((ntiles + kWaves - 1) / kWaves <= kShort)
+    if ((ntiles + W - 1) / W <= kShort)
         stream(std::integral_constant<int, kShort>{});
     else
         stream(std::integral_constant<int, NST>{});
@@ -715,9 +731,9 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     // over the tiles, every wave must be done reading its tiles first)
     l_run = col_sum4(l_run);
     if constexpr (Gm::COMB_OFF == 0) __syncthreads();
-    float* cm = reinterpret_cast<float*>(smem + Gm::COMB_OFF);  // [kWaves][16]
-    float* cl = cm + kWaves * 16;                          // [kWaves][16]
-    float* co = cl + kWaves * 16;                          // [kWaves][16][CROW]
+    float* cm = reinterpret_cast<float*>(smem + Gm::COMB_OFF);  // [W][16]
+    float* cl = cm + W * 16;                          // [W][16]
+    float* co = cl + W * 16;                          // [W][16][CROW]
     if (kb == 0) {
         cm[wave * 16 + col] = m_run;
         cl[wave * 16 + col] = l_run;
@@ -731,15 +747,15 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
     const int gcount = min(16, p.G - gb * 16);
     const __amdgpu_buffer_rsrc_t rpo = coherent_rsrc(p.part_o, 0x7fffffff);
     const __amdgpu_buffer_rsrc_t rpml = coherent_rsrc(p.part_ml, 0x7fffffff);
-    for (int idx = tid; idx < gcount * (D / 4); idx += kThreads) {
+    for (int idx = tid; idx < gcount * (D / 4); idx += NT) {
         const int gg = idx / (D / 4), d4 = idx % (D / 4);
         float M = cm[gg];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, cm[w * 16 + gg]);
+        for (int w = 1; w < W; ++w) M = fmaxf(M, cm[w * 16 + gg]);
         float L = 0.0f;
         f4 O = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float df = cm[w * 16 + gg] - M;
             const float wt = df < kCut2 ? 0.0f : exp2_fast(df);
             L += wt * cl[w * 16 + gg];
@@ -794,7 +810,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
                           (unsigned)nsp - 1u;
             __syncthreads();
             if (!is_last) return;
-            merge_any<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp);
+            merge_any<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp);
             write_q();  // every workgroup of the group has read q by now
             if (tid == 0) __hip_atomic_store(cnt + kCounterStride / 2, base + (unsigned)nsp, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
@@ -804,7 +820,7 @@ __global__ __launch_bounds__(kThreads, PAGED ? kPagedWgsPerCu : 2) void fa_decod
         if (mk < 0) return;
         if (tid == 0) wait_count(cnt, base + (unsigned)nsp);
         __syncthreads();
-        merge_slice<D>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
+        merge_slice<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
         if (mk == 0) {
             write_q();  // every workgroup of the group has read q by now
             if (tid == 0) __hip_atomic_store(cnt + kCounterStride / 2, base + (unsigned)nsp, __ATOMIC_RELAXED,
@@ -820,7 +836,7 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
     const int S = context_len(p, row / p.Hq, PAGED);
     const int nsp = split_count(S, p.min_chunk, p.max_splits);
     if (p.single || nsp <= 1) return;  // the decode kernel wrote the output
-    merge_any<D>(p, (size_t)row, 1, nsp);
+    merge_any<D, kThreads>(p, (size_t)row, 1, nsp);
 }
 
 template <int D, bool PAGED, bool Q8>
@@ -828,14 +844,16 @@ int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
     // fixed mergers while the whole grid can be resident at once, else the last arriver merges
-    const size_t resident = kCus * (PAGED ? kPagedWgsPerCu : 2);
+    const size_t resident = kCus * wgs_per_cu(PAGED, Q8);
     p.merge_slices = (size_t)grid.x * grid.y * grid.z <= resident ? kMergeSlices : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
-        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid,
+                           dim3(waves_for(PAGED, Q8) * 64), 0, stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, false>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, false>), grid,
+                       dim3(waves_for(PAGED, Q8) * 64), 0, stream, p);
     if (hipGetLastError() != hipSuccess) return -1;
     if (!p.single && !p.counters) {
         hipLaunchKernelGGL((fa_merge_kernel<D, PAGED>), dim3(batch * p.Hq), dim3(kThreads), 0, stream, p);
