@@ -390,8 +390,10 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             append_row = (S - 1) - (start + last_tile * kTile);
         }
     }
-    // The inputs other than the cache (q, the RoPE table entries, the new row): issued after
-    // the first K/V tiles, so that those, the longest wait, start first.
+    // The inputs other than the cache (q, the RoPE table entries, the new row). Decode only:
+    // issued after the first K/V tiles, so that those, the longest wait, start first. Step:
+    // issued before them, because vector loads complete in order: the q rotation waits for
+    // these loads only, and runs while the first tiles are in flight.
     auto load_inputs = [&]() __attribute__((always_inline)) {
         const uint16_t* qrow = p.q + ((size_t)b * p.Hq + (gvalid ? head : kvh * p.G)) * D;
 #pragma unroll
@@ -706,11 +708,12 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         constexpr int N = decltype(n_tag)::value;
         Stage st[N];
         const int groups = (my_tiles + N - 1) / N;
+        if (ROPE) load_inputs();
         if (groups > 0) {
 #pragma unroll
             for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * W);
         }
-        load_inputs();
+        if (!ROPE) load_inputs();
         prepare();
         for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
