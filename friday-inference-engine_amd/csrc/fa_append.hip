@@ -26,17 +26,26 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= (p.Hq + p.Hkv) * cpp) return;
     const int h = idx / cpp, c = idx - h * cpp;
-    const int pos = PAGED ? p.seq_lens[t] - 1 : (p.d_pos ? *p.d_pos : p.pos) + t;
-    if (pos < 0 || pos >= p.max_ctx) return;
-    const float2* cs = reinterpret_cast<const float2*>(p.table) + (size_t)pos * hd2;
     const int kv_dim = p.Hkv * p.D;
     const bool is_k = h >= p.Hq;
     _Float16* x = is_k ? reinterpret_cast<_Float16*>(p.k) + (size_t)t * kv_dim + (h - p.Hq) * p.D
                        : reinterpret_cast<_Float16*>(p.q) + (size_t)t * p.Hq * p.D + h * p.D;
     // element offsets of the chunk (and, NeoX, its partner chunk)
     const int e0 = 8 * c, e1 = p.neox ? hd2 + 8 * c : 8 * c;
-    h8 a = *reinterpret_cast<const h8*>(x + e0);
-    h8 bv = *reinterpret_cast<const h8*>(x + e1);
+    // the loads whose addresses do not depend on the position go out before it is read, so
+    // their latency overlaps the position's round trip
+    const h8 a = *reinterpret_cast<const h8*>(x + e0);
+    const h8 bv = *reinterpret_cast<const h8*>(x + e1);
+    const bool store_kv = is_k && p.k_dst;
+    const _Float16* vs = reinterpret_cast<const _Float16*>(p.v) + (size_t)t * kv_dim + (h - p.Hq) * p.D;
+    h8 v0 = h8{0, 0, 0, 0, 0, 0, 0, 0}, v1 = v0;
+    if (store_kv) {
+        v0 = *reinterpret_cast<const h8*>(vs + e0);
+        if (p.neox) v1 = *reinterpret_cast<const h8*>(vs + e1);
+    }
+    const int pos = PAGED ? p.seq_lens[t] - 1 : (p.d_pos ? *p.d_pos : p.pos) + t;
+    if (pos < 0 || pos >= p.max_ctx) return;
+    const float2* cs = reinterpret_cast<const float2*>(p.table) + (size_t)pos * hd2;
     h8 ra, rb;
     if (p.neox) {
 #pragma unroll
@@ -60,7 +69,7 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
     }
     *reinterpret_cast<h8*>(x + e0) = ra;
     if (p.neox) *reinterpret_cast<h8*>(x + e1) = rb;
-    if (is_k && p.k_dst) {
+    if (store_kv) {
         size_t row;
         if (PAGED) {
             const int phys = p.block_table[(size_t)t * p.bt_stride + (pos >> 4)];
@@ -71,12 +80,11 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
         const size_t off = row * kv_dim + (size_t)(h - p.Hq) * p.D;
         _Float16* kd = reinterpret_cast<_Float16*>(p.k_dst) + off;
         _Float16* vd = reinterpret_cast<_Float16*>(p.v_dst) + off;
-        const _Float16* vs = reinterpret_cast<const _Float16*>(p.v) + (size_t)t * kv_dim + (h - p.Hq) * p.D;
         *reinterpret_cast<h8*>(kd + e0) = ra;
-        *reinterpret_cast<h8*>(vd + e0) = *reinterpret_cast<const h8*>(vs + e0);
+        *reinterpret_cast<h8*>(vd + e0) = v0;
         if (p.neox) {
             *reinterpret_cast<h8*>(kd + e1) = rb;
-            *reinterpret_cast<h8*>(vd + e1) = *reinterpret_cast<const h8*>(vs + e1);
+            *reinterpret_cast<h8*>(vd + e1) = v1;
         }
     }
 }
