@@ -8,15 +8,18 @@
 // exp(s - max) cut to 0 below -50, fp32 accumulation, output NaN -> 0, clamped
 // to +-65504, rounded to fp16. Only the order of the fp32 additions differs.
 //
-// Data flow of one wave per 32-position tile:
-//   HBM --(coalesced 16 B loads, one tile ahead in registers)--> LDS (padded rows)
-//   S^T[32 x 16] = K[32 x D] . Q^T[D x 16]     v_mfma_f32_16x16x32_f16, K from LDS
+// Data flow of one wave per 16-position tile:
+//   HBM --(coalesced 16 B loads through a per-tile buffer descriptor, the next tile in
+//          flight in registers)--> the wave's LDS tile (padded rows; int8 rows are
+//          dequantised to fp16 on the way)
+//   S^T[16 x 16] = K[16 x D] . Q^T[D x 16]     v_mfma_f32_16x16x32_f16, K from LDS
 //   online softmax on S^T in registers: every lane owns one query head (l % 16)
-//   O^T[D x 16] += V^T[D x 32] . P^T[32 x 16]   P stays in the registers the
-//                                               S^T MFMA produced it in; V^T read
-//                                               column-wise from LDS
-// The four waves of a workgroup take interleaved tiles of the split and are
-// merged through LDS; splits are merged by fa_merge_kernel (log-sum-exp).
+//   O^T[D x 16] += V^T[D x 16] . P^T[16 x 16]   P stays in the registers the S^T MFMA
+//                                               produced it in; V^T by transposing
+//                                               LDS reads (ds_read_b64_tr_b16)
+// The waves of a workgroup take interleaved tiles of the split and combine through LDS;
+// the splits are merged (log-sum-exp) by the last workgroups of each group in the same
+// launch (fused merge) or by fa_merge_kernel (the reference's two-launch form).
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
@@ -729,7 +732,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     else
         stream(std::integral_constant<int, NST>{});
 
-    // ---- combine the four waves of the workgroup through LDS ----
+    // ---- combine the W waves of the workgroup through LDS ----
     // (with a region of its own, each wave writes its state without waiting for the others;
     // over the tiles, every wave must be done reading its tiles first)
     l_run = col_sum4(l_run);
