@@ -6,15 +6,21 @@
 // the running max, fp32 accumulation, output NaN -> 0, clamp, RNE fp16. Row t
 // equals decode attention with S = p0 + t + 1 up to the order of fp32 additions.
 //
-// Work decomposition: rows r = t * G + g of one kv head (all query heads of the
-// GQA group for every token share its K/V). A workgroup owns 128 rows (4 waves
-// x 32) and streams the kv head's K/V in 32-position tiles through LDS, shared
-// by the four waves:
+// Work decomposition: rows r = t * G + g of one kv head (all query heads of the GQA group
+// for every token share its K/V).
+// fa_prefill_dma_kernel (every fp16 / bf16 call, and int8 calls with 4-byte aligned scale
+// arrays): a workgroup of eight waves owns up to six 16-row tiles in two groups of four
+// waves; stages of 128 keys are copied global -> LDS by global_load_lds_dwordx4 (two
+// stage buffers, the next stage in flight during this one's MFMAs), each wave of a group
+// takes 32 keys of the stage for all of its group's row tiles, and the four key slices'
+// softmax states merge through LDS at the end. int8 stages are copied raw and decoded to
+// fp16 in LDS by the whole workgroup before the MFMAs.
+// fa_prefill_kernel (int8 scale arrays off 4-byte alignment): 128 rows (4 waves x 32),
+// K/V staged through registers in 32-position tiles:
 //   K tile row-major            -> A operand of S^T = K Q^T   (ds_read_b128)
 //   V tile transposed, with the positions of one lane block stored together
 //                               -> A operand of O^T += V^T P^T (ds_read_b128)
-// Each wave keeps Q^T, O^T and the softmax state of its 32 rows in registers;
-// every K/V fragment read from LDS feeds two MFMAs (two 16-row tiles).
+// Both keep Q^T, O^T and the softmax state in registers.
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
