@@ -8,19 +8,13 @@
 //
 // Work decomposition: rows r = t * G + g of one kv head (all query heads of the GQA group
 // for every token share its K/V).
-// fa_prefill_dma_kernel (every fp16 / bf16 call, and int8 calls with 4-byte aligned scale
-// arrays): a workgroup of eight waves owns up to six 16-row tiles in two groups of four
-// waves; stages of 128 keys are copied global -> LDS by global_load_lds_dwordx4 (two
-// stage buffers, the next stage in flight during this one's MFMAs), each wave of a group
-// takes 32 keys of the stage for all of its group's row tiles, and the four key slices'
-// softmax states merge through LDS at the end. int8 stages are copied raw and decoded to
-// fp16 in LDS by the whole workgroup before the MFMAs.
-// fa_prefill_kernel (int8 scale arrays off 4-byte alignment): 128 rows (4 waves x 32),
-// K/V staged through registers in 32-position tiles:
-//   K tile row-major            -> A operand of S^T = K Q^T   (ds_read_b128)
-//   V tile transposed, with the positions of one lane block stored together
-//                               -> A operand of O^T += V^T P^T (ds_read_b128)
-// Both keep Q^T, O^T and the softmax state in registers.
+// fa_prefill_dma_kernel: a workgroup of eight waves owns up to six 16-row tiles in two
+// groups of four waves; stages of 128 keys are copied global -> LDS by
+// global_load_lds_dwordx4 (two stage buffers, the next stage in flight during this one's
+// MFMAs), each wave of a group takes 32 keys of the stage for all of its group's row tiles,
+// and the four key slices' softmax states merge through LDS at the end. Q^T, O^T and the
+// softmax state stay in registers. int8 caches: every wave copies its share of the next
+// stage's codes raw into LDS and decodes it to fp16 itself while this stage's MFMAs run.
 #include "fa_common.hpp"
 #include "fa_internal.hpp"
 
@@ -31,226 +25,7 @@
 namespace fa {
 namespace {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = kPfWaves * 64;
-constexpr int kPfRT = 2;                        // 16-row tiles per wave
-constexpr int kPfRowsWave = 16 * kPfRT;
-constexpr int kPfRowsWG = kPfRowsWave * kPfWaves;  // 128
-constexpr int kPfTile = 32;                     // key positions per tile
-
-template <int D, bool Q8>
-struct PfGeo {
-    static constexpr int KROW = D * 2 + 16;              // K tile row stride (bytes)
-    static constexpr int VTROW = kPfTile * 2 + 16;       // V^T row stride (bytes), one row per d
-    static constexpr int K_LDS = kPfTile * KROW;
-    static constexpr int V_LDS = D * VTROW;
-    static constexpr int KSTEPS = D / 32;
-    static constexpr int DTILES = D / 16;
-    static constexpr int ROWB = Q8 ? D : 2 * D;          // cache bytes per kv-head row
-    static constexpr int CPR = ROWB / 16;                // 16 B chunks per row
-    static constexpr int RPR = kPfThreads / CPR;         // rows per round
-    static constexpr int ROUNDS = (kPfTile + RPR - 1) / RPR;
-};
-
-// V^T column of tile position p: the 8 positions that lane block kb feeds to one
-// MFMA (p = kb*4+j and 16+kb*4+j, j < 4) are stored contiguously.
-__device__ __forceinline__ int vt_col(int p) { return ((p & 15) >> 2) * 8 + (p >> 4) * 4 + (p & 3); }
-
-template <int D, bool Q8>
-__global__ __launch_bounds__(kPfThreads) void fa_prefill_kernel(PrefillParams p) {
-    using Gm = PfGeo<D, Q8>;
-    __shared__ __align__(16) unsigned char s_k[Gm::K_LDS];
-    __shared__ __align__(16) unsigned char s_vt[Gm::V_LDS];
-
-    const int R = p.T * p.G;
-    const int rtile = gridDim.x - 1 - blockIdx.x;  // heavier (later) rows first
-    const int kvh = blockIdx.y;
-    const int row0 = rtile * kPfRowsWG;
-    const int p0 = *p.d_pos0;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int col = lane & 15, kb = lane >> 4;
-    const int qd = p.Hq * D;
-    const int kv_dim = p.Hkv * D;
-
-    // rows of this lane (one per 16-row tile) and their causal limits
-    int lim[kPfRT];
-    h8 qf[kPfRT][Gm::KSTEPS];
-#pragma unroll
-    for (int rt = 0; rt < kPfRT; ++rt) {
-        const int r = row0 + wave * kPfRowsWave + rt * 16 + col;
-        const bool valid = r < R;
-        const int t = valid ? r / p.G : 0, g = valid ? r % p.G : 0;
-        lim[rt] = valid ? p0 + t : -1;
-        const uint16_t* qrow = p.q + (size_t)t * qd + (size_t)(kvh * p.G + g) * D;
-#pragma unroll
-        for (int s = 0; s < Gm::KSTEPS; ++s) {
-            u4 raw = valid ? *reinterpret_cast<const u4*>(qrow + s * 32 + kb * 8) : u4{0, 0, 0, 0};
-            qf[rt][s] = *reinterpret_cast<h8*>(&raw);
-        }
-    }
-    const int wg_last = min(row0 + kPfRowsWG, R) - 1;
-    const int wv_last = min(row0 + wave * kPfRowsWave + kPfRowsWave, R) - 1;
-    const int kend = p0 + wg_last / p.G + 1;                              // keys [0, kend) for the workgroup
-    const int wend = wv_last >= row0 + wave * kPfRowsWave ? p0 + wv_last / p.G + 1 : 0;  // for this wave
-    const int ntiles = (kend + kPfTile - 1) / kPfTile;
-
-    float m_run[kPfRT], l_run[kPfRT];
-    f4 o[kPfRT][Gm::DTILES];
-#pragma unroll
-    for (int rt = 0; rt < kPfRT; ++rt) {
-        m_run[rt] = kNegBig;
-        l_run[rt] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < Gm::DTILES; ++i) o[rt][i] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * Gm::ROWB;
-    const char* vbase = static_cast<const char*>(p.v) + (size_t)kvh * Gm::ROWB;
-    const size_t rowb = (size_t)kv_dim * (Q8 ? 1 : 2);
-    const int lrow = tid / Gm::CPR, lchunk = tid % Gm::CPR;
-    u4 kr[Gm::ROUNDS], vr[Gm::ROUNDS];
-    float ksc[Gm::ROUNDS], vsc[Gm::ROUNDS];
-
-    auto load_tile = [&](int kt) {
-#pragma unroll
-        for (int r = 0; r < Gm::ROUNDS; ++r) {
-            const int pr = r * Gm::RPR + lrow;
-            const int pos = kt * kPfTile + pr;
-            if (pr < kPfTile && pos < kend) {
-                kr[r] = *(reinterpret_cast<const u4*>(kbase + (size_t)pos * rowb) + lchunk);
-                vr[r] = *(reinterpret_cast<const u4*>(vbase + (size_t)pos * rowb) + lchunk);
-                if (Q8) {
-                    const size_t si = ((size_t)pos * kv_dim + (size_t)kvh * D + lchunk * 16) / 32;
-                    ksc[r] = (float)*reinterpret_cast<const _Float16*>(p.k_scale + si);
-                    vsc[r] = (float)*reinterpret_cast<const _Float16*>(p.v_scale + si);
-                }
-            } else {
-                kr[r] = u4{0, 0, 0, 0};
-                vr[r] = u4{0, 0, 0, 0};
-                if (Q8) { ksc[r] = 0.f; vsc[r] = 0.f; }
-            }
-        }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int r = 0; r < Gm::ROUNDS; ++r) {
-            const int pr = r * Gm::RPR + lrow;
-            if (pr >= kPfTile) continue;
-            h8 kv[2], vv[2];
-            int nparts;
-            if (Q8) {
-                const int8_t* kc = reinterpret_cast<const int8_t*>(&kr[r]);
-                const int8_t* vc = reinterpret_cast<const int8_t*>(&vr[r]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    kv[0][j] = (_Float16)((float)kc[j] * ksc[r]);
-                    kv[1][j] = (_Float16)((float)kc[8 + j] * ksc[r]);
-                    vv[0][j] = (_Float16)((float)vc[j] * vsc[r]);
-                    vv[1][j] = (_Float16)((float)vc[8 + j] * vsc[r]);
-                }
-                nparts = 2;
-            } else {
-                kv[0] = *reinterpret_cast<h8*>(&kr[r]);
-                vv[0] = *reinterpret_cast<h8*>(&vr[r]);
-                nparts = 1;
-            }
-            const int d0 = lchunk * (Q8 ? 16 : 8);
-            const int c = vt_col(pr);
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-                if (part >= nparts) break;
-                *reinterpret_cast<h8*>(s_k + pr * Gm::KROW + (d0 + part * 8) * 2) = kv[part];
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    *reinterpret_cast<_Float16*>(s_vt + (d0 + part * 8 + j) * Gm::VTROW + c * 2) = vv[part][j];
-            }
-        }
-    };
-
-    if (ntiles > 0) load_tile(0);
-    for (int kt = 0; kt < ntiles; ++kt) {
-        store_tile();
-        __syncthreads();
-        if (kt + 1 < ntiles) load_tile(kt + 1);
-        const int tbase = kt * kPfTile;
-        if (tbase < wend) {
-            // S^T[pos][row] for two 16-position m-tiles x two 16-row tiles
-            f4 sacc[kPfRT][2];
-#pragma unroll
-            for (int rt = 0; rt < kPfRT; ++rt) sacc[rt][0] = sacc[rt][1] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-                for (int s = 0; s < Gm::KSTEPS; ++s) {
-                    const h8 a = *reinterpret_cast<const h8*>(s_k + (mt * 16 + col) * Gm::KROW + (s * 32 + kb * 8) * 2);
-#pragma unroll
-                    for (int rt = 0; rt < kPfRT; ++rt) sacc[rt][mt] = mfma16x16x32(a, qf[rt][s], sacc[rt][mt]);
-                }
-            }
-            h8 pf[kPfRT];
-            float alpha[kPfRT];
-#pragma unroll
-            for (int rt = 0; rt < kPfRT; ++rt) {
-                float sc[8];
-                float mx = kNegBig;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int mt = j >> 2, i = j & 3;
-                    float x = sacc[rt][mt][i] * p.scale2;
-                    if (__builtin_isnan(x)) x = kNegBig;
-                    const bool valid = tbase + mt * 16 + kb * 4 + i <= lim[rt];
-                    sc[j] = valid ? x : -__builtin_inff();
-                    mx = fmaxf(mx, sc[j]);
-                }
-                mx = wave_max_xor(mx, 16);
-                mx = wave_max_xor(mx, 32);
-                const float m_new = fmaxf(m_run[rt], mx);
-                const float da = m_run[rt] - m_new;
-                alpha[rt] = da < kCut2 ? 0.0f : exp2_fast(da);
-                float psum = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float df = sc[j] - m_new;
-                    const float e = df < kCut2 ? 0.0f : exp2_fast(df);
-                    const _Float16 eh = (_Float16)e;
-                    pf[rt][j] = eh;
-                    psum += (float)eh;
-                }
-                l_run[rt] = l_run[rt] * alpha[rt] + psum;
-                m_run[rt] = m_new;
-            }
-#pragma unroll
-            for (int dt = 0; dt < Gm::DTILES; ++dt) {
-                const h8 va = *reinterpret_cast<const h8*>(s_vt + (dt * 16 + col) * Gm::VTROW + kb * 16);
-#pragma unroll
-                for (int rt = 0; rt < kPfRT; ++rt) o[rt][dt] = mfma16x16x32(va, pf[rt], o[rt][dt] * alpha[rt]);
-            }
-        }
-        __syncthreads();
-    }
-
-    // epilogue: lane holds O^T[d = dt*16 + kb*4 + i][row col] of each row tile
-#pragma unroll
-    for (int rt = 0; rt < kPfRT; ++rt) {
-        float L = wave_sum_xor(l_run[rt], 16);
-        L = wave_sum_xor(L, 32);
-        const int r = row0 + wave * kPfRowsWave + rt * 16 + col;
-        if (r >= R) continue;
-        const int t = r / p.G, g = r % p.G;
-        _Float16* orow = reinterpret_cast<_Float16*>(p.out) + (size_t)t * qd + (size_t)(kvh * p.G + g) * D;
-#pragma unroll
-        for (int dt = 0; dt < Gm::DTILES; ++dt) {
-            h4 v;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = out_half(L > 1e-12f ? o[rt][dt][i] / L : 0.0f);
-            *reinterpret_cast<h4*>(orow + dt * 16 + kb * 4) = v;
-        }
-    }
-}
-
-
-// ---------------------------------------------------------------------------
-// fp16 caches: LDS-DMA pipeline.
+// LDS-DMA pipeline.
 //
 // A workgroup owns RA + RB 16-row tiles of one kv head (rows r = t*G + g) and streams
 // the head's keys in stages of 128 positions through a two-stage LDS ring that
@@ -259,10 +34,12 @@ __global__ __launch_bounds__(kPfThreads) void fa_prefill_kernel(PrefillParams p)
 // group, each of the four waves takes 32 keys of every stage for all of the group's
 // row tiles, so every K/V fragment it reads from LDS feeds RA (or RB) MFMAs; the four
 // waves' softmax states are merged through LDS at the end. With 128 KB of LDS per
-// workgroup a CU runs one workgroup, i.e. two waves per SIMD (one of each group): while
-// one wave runs its softmax on the vector unit, the other can issue its MFMAs. K and V rows stay row-major in LDS with the 16-byte chunks of row
-// r stored at slot chunk ^ (r % CPR), which makes the MFMA operand reads free of bank
+// workgroup (160 KB with the int8 raw codes) a CU runs one workgroup, i.e. two waves per
+// SIMD (one of each group): while one wave runs its softmax on the vector unit, the other
+// can issue its MFMAs. K and V rows stay row-major in LDS with the 16-byte chunks of row
+// r stored at slot chunk ^ swz(r), which makes the MFMA operand reads free of bank
 // conflicts; V^T comes from the transposing LDS read (ds_read_b64_tr_b16).
+
 constexpr int kP2Slices = 4;                // key slices of a stage (one wave each per group)
 constexpr int kP2Groups = 2;                // row-tile groups sharing every stage
 constexpr int kP2Waves = kP2Slices * kP2Groups;
@@ -294,23 +71,19 @@ struct P2Geo {
     static __device__ __forceinline__ int swz(int r) { return ((r & (CPR / 2 - 1)) << 1) | ((r / (CPR / 2)) & 1); }
 };
 
-// int8 caches: raw stage = the codes of K and V (row-major, kP2KS rows of D bytes each)
-// followed by their fp16 scales (D/32 per row), copied by DMA as they lie in memory.
+// int8 caches: each wave copies the codes of stage rows [16 w, 16 w + 16) of K and of V
+// into a raw region of its own (row-major, D bytes per row) and decodes them itself, with
+// the fp16 scales of its lanes' chunks loaded into registers.
 template <int D>
 struct P2RawGeo {
     static constexpr int ROWB = D;                     // code bytes of one row
-    static constexpr int CPR = ROWB / 16;              // 16-byte chunks per row
-    static constexpr int RPI = 64 / CPR;               // rows per wave DMA instruction
-    static constexpr int PART = kP2KS * ROWB;          // codes of K (or V) in a stage
-    static constexpr int SROWB = D / 16;               // scale bytes of one row
-    static constexpr int SDW = SROWB / 4;              // scale dwords of one row
-    static constexpr int SPART = kP2KS * SROWB;        // scales of K (or V) in a stage
-    static constexpr int NI = kP2KS / RPI / kP2DmaWaves;  // code DMA instructions per wave per tensor
-    static constexpr int SI = SPART / 4 / 64;          // scale DMA instructions per tensor (one per wave)
-    static constexpr int RAW = 2 * PART + 2 * SPART;
-    static constexpr int NCH = 2 * kP2KS * CPR;        // 16-code chunks of a stage (K and V)
-    static_assert(SI >= 1 && SI <= kP2DmaWaves && SPART % 256 == 0, "scale copy shape");
-    static_assert(NCH % kP2Threads == 0, "decode shape");
+    static constexpr int CPR = ROWB / 16;              // 16-code chunks per row
+    static constexpr int RPI = 64 / CPR;               // rows per wave copy instruction
+    static constexpr int WROWS = kP2KS / kP2Waves;     // stage rows per wave
+    static constexpr int NI = WROWS / RPI;             // copy instructions per wave and tensor
+    static constexpr int WAVE = 2 * WROWS * ROWB;      // raw bytes per wave (K rows, then V rows)
+    static constexpr int RAW = kP2Waves * WAVE;
+    static_assert(NI >= 1 && NI * RPI == WROWS, "copy shape");
 };
 
 // One wave-wide global -> LDS copy (global_load_lds_dwordx4): lane l moves 16 bytes
@@ -330,15 +103,13 @@ __device__ __forceinline__ void dma4(const char* base, uint32_t off, lds_u8* lds
                  : "memory");
 }
 
-// Bytes of the LDS buffers: fp16 caches use two fp16 stages (stage0, stage1); int8
-// caches use one fp16 stage (stage0, decoded from the raw stage in use) and two raw
-// stages (stage1, stage2), the first also holding group 1's merge area.
+// Bytes of the LDS buffers: two fp16 stages (stage0, stage1); int8 caches add the raw
+// codes of one stage (stage2): 64 + 64 + 32 KiB at D = 128, the whole LDS of a CU.
 template <int D, bool Q8>
 struct P2Lds {
     static constexpr int B0 = P2Geo<D>::STAGE;
-    static constexpr int RAWB = P2RawGeo<D>::RAW > P2Geo<D>::CREG_BYTES ? P2RawGeo<D>::RAW : P2Geo<D>::CREG_BYTES;
-    static constexpr int B1 = Q8 ? RAWB : P2Geo<D>::STAGE;
-    static constexpr int B2 = Q8 ? RAWB : 16;
+    static constexpr int B1 = P2Geo<D>::STAGE;
+    static constexpr int B2 = Q8 ? P2RawGeo<D>::RAW : 16;
 };
 
 template <int D, int RA, int RB, bool Q8, bool BF>
@@ -401,31 +172,21 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     // first token of the group's first tile: slices up to it need no causal mask
     const int grp_lo = row0 < R ? p0 + row0 / p.G : INT_MAX;
 
-    // DMA of one stage: wave w moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K and V parts
+    // fp16 stage copy: wave w < kP2DmaWaves moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K and
+    // V parts, each 16-byte chunk to its swizzled slot
     constexpr int CROWB = Q8 ? Rg::ROWB : Gm::ROWB;  // cache bytes of one kv-head row
-    constexpr int CCPR = Q8 ? Rg::CPR : Gm::CPR;
-    constexpr int CRPI = Q8 ? Rg::RPI : Gm::RPI;
-    constexpr int CNI = Q8 ? Rg::NI : Gm::NI;
     const size_t rowb = (size_t)p.Hkv * CROWB;
     const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * CROWB;
     const char* vbase = static_cast<const char*>(p.v) + (size_t)kvh * CROWB;
-    const int drow = lane / CCPR, dslot = lane % CCPR;
-    // this lane's byte offsets (row, chunk) within a stage, one per DMA instruction; fp16
-    // rows land with their chunks swizzled, int8 rows as they are (the decode pass swizzles)
-    uint32_t doff[CNI];
+    const int drow = lane / Gm::CPR, dslot = lane % Gm::CPR;
+    uint32_t doff[Gm::NI];
 #pragma unroll
-    for (int i = 0; i < CNI; ++i) {
-        const int r = (wave * CNI + i) * CRPI + drow;
-        doff[i] = (uint32_t)(r * (int)rowb + (Q8 ? dslot : (dslot ^ Gm::swz(r))) * 16);
+    for (int i = 0; i < Gm::NI; ++i) {
+        const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
+        doff[i] = (uint32_t)(r * (int)rowb + (dslot ^ Gm::swz(r)) * 16);
     }
-    lds_u8* const lds0 = (lds_u8*)(Q8 ? stage1 : stage0);
-    lds_u8* const lds1 = (lds_u8*)(Q8 ? stage2 : stage1);
-    // int8 scales: the row's D/32 fp16 scales are contiguous ([pos][kv_dim/32] layout)
-    const size_t srowb = (size_t)p.Hkv * Rg::SROWB;
-    const char* ksbase = reinterpret_cast<const char*>(p.k_scale) + (size_t)kvh * Rg::SROWB;
-    const char* vsbase = reinterpret_cast<const char*>(p.v_scale) + (size_t)kvh * Rg::SROWB;
-    const int srow = (wave * 64 + lane) / Rg::SDW;  // scale row of this lane's dword (waves < SI)
-    const uint32_t soff = (uint32_t)(srow * (int)srowb + ((wave * 64 + lane) % Rg::SDW) * 4);
+    lds_u8* const lds0 = (lds_u8*)stage0;
+    lds_u8* const lds1 = (lds_u8*)stage1;
     auto issue = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
         if (wave >= kP2DmaWaves) return;
         lds_u8* st = decltype(stage_tag)::value ? lds1 : lds0;
@@ -434,69 +195,66 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         const char* kt = kbase + tile0;
         const char* vt = vbase + tile0;
         const int rmax = kend - 1 - tile * kP2KS;  // rows past it re-read the last key
-        constexpr int VOFF = Q8 ? Rg::PART : Gm::STAGE_K;  // V part of the stage
         if (rmax >= kP2KS - 1) {
 #pragma unroll
-            for (int i = 0; i < CNI; ++i) {
-                lds_u8* l = st + (wave * CNI + i) * CRPI * CROWB;
+            for (int i = 0; i < Gm::NI; ++i) {
+                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
                 dma16(kt, doff[i], l);
-                dma16(vt, doff[i], l + VOFF);
+                dma16(vt, doff[i], l + Gm::STAGE_K);
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < CNI; ++i) {
-                const int r = (wave * CNI + i) * CRPI + drow;
-                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (Q8 ? dslot : (dslot ^ Gm::swz(r))) * 16);
-                lds_u8* l = st + (wave * CNI + i) * CRPI * CROWB;
+            for (int i = 0; i < Gm::NI; ++i) {
+                const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
+                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (dslot ^ Gm::swz(r)) * 16);
+                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
                 dma16(kt, off, l);
-                dma16(vt, off, l + VOFF);
-            }
-        }
-        if constexpr (Q8) {
-            if (wave < Rg::SI) {
-                const size_t stile0 = (size_t)tile * kP2KS * srowb;
-                const uint32_t off = rmax >= kP2KS - 1
-                                         ? soff
-                                         : (uint32_t)(min(srow, rmax) * (int)srowb + ((wave * 64 + lane) % Rg::SDW) * 4);
-                lds_u8* l = st + 2 * Rg::PART + wave * 256;
-                dma4(ksbase + stile0, off, l);
-                dma4(vsbase + stile0, off, l + Rg::SPART);
+                dma16(vt, off, l + Gm::STAGE_K);
             }
         }
     };
-    // int8: the raw stage -> fp16 stage0 (same layout as the fp16 DMA: chunk slot
-    // chunk ^ (row % CPR)); each 16-code chunk becomes two fp16 chunks (dequant16)
-    auto decode = [&](const unsigned char* raw) __attribute__((always_inline)) {
-        constexpr int NIT = Rg::NCH / kP2Threads;
-        // chunks whose LDS reads are issued together: their latencies overlap; a larger batch
-        // spills at the largest row-tile share
-        constexpr int NB = 2;
-        static_assert(NIT % NB == 0, "decode batches");
-#pragma unroll 1
-        for (int it0 = 0; it0 < NIT; it0 += NB) {
-            u4 q[NB];
-            float sc[NB];
+    // int8 stage copy: every wave moves its own rows [w*WROWS, (w+1)*WROWS) of K and V into
+    // its raw region (lane l's 16 codes at + 16 l of each instruction) and loads the fp16
+    // scales of the chunks its lanes decode into registers
+    const int qrow = lane / Rg::CPR, qch = lane % Rg::CPR;
+    lds_u8* const rawl = (lds_u8*)stage2 + wave * Rg::WAVE;
+    const int sdim = p.Hkv * (D / 32);  // scales per cache position
+    const uint16_t* ksc = p.k_scale + (size_t)kvh * (D / 32) + (qch >> 1);
+    const uint16_t* vsc = p.v_scale + (size_t)kvh * (D / 32) + (qch >> 1);
+    uint16_t qsk[Rg::NI], qsv[Rg::NI];
+    auto issue_q8 = [&](int tile) __attribute__((always_inline)) {
+        const size_t tile0 = (size_t)tile * kP2KS * rowb;
+        const char* kt = kbase + tile0;
+        const char* vt = vbase + tile0;
+        const int rmax = kend - 1 - tile * kP2KS;  // rows past it re-read the last key
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const int idx = (it0 + b) * kP2Threads + tid;
-                const int ts = idx / (kP2KS * Rg::CPR);  // 0: K, 1: V
-                const int rem = idx % (kP2KS * Rg::CPR);
-                const int r = rem / Rg::CPR, c = rem % Rg::CPR;
-                q[b] = *reinterpret_cast<const u4*>(raw + ts * Rg::PART + rem * 16);
-                sc[b] = (float)*reinterpret_cast<const _Float16*>(raw + 2 * Rg::PART + ts * Rg::SPART +
-                                                                   r * Rg::SROWB + (c >> 1) * 2);
-            }
+        for (int i = 0; i < Rg::NI; ++i) {
+            const int r = min(wave * Rg::WROWS + i * Rg::RPI + qrow, rmax);
+            const uint32_t off = (uint32_t)(r * (int)rowb + qch * 16);
+            dma16(kt, off, rawl + i * 1024);
+            dma16(vt, off, rawl + Rg::WROWS * Rg::ROWB + i * 1024);
+            const size_t pos = (size_t)tile * kP2KS + r;
+            qsk[i] = ksc[pos * sdim];
+            qsv[i] = vsc[pos * sdim];
+        }
+    };
+    // int8: this wave's raw rows -> the fp16 stage `dst` (the fp16 copy's layout: chunk c
+    // of row r at slot c ^ swz(r)); each 16-code chunk becomes two fp16 chunks (dequant16).
+    // Only this wave's own copies are read, so its own vmcnt wait covers them.
+    auto decode_q8 = [&](unsigned char* dst) __attribute__((always_inline)) {
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const int idx = (it0 + b) * kP2Threads + tid;
-                const int ts = idx / (kP2KS * Rg::CPR);
-                const int rem = idx % (kP2KS * Rg::CPR);
-                const int r = rem / Rg::CPR, c = rem % Rg::CPR;
+        for (int i = 0; i < Rg::NI; ++i) {
+            const int r = wave * Rg::WROWS + i * Rg::RPI + qrow;
+#pragma unroll
+            for (int ts = 0; ts < 2; ++ts) {
+                const u4 q = *reinterpret_cast<const u4*>((const unsigned char*)rawl + ts * Rg::WROWS * Rg::ROWB +
+                                                          i * 1024 + lane * 16);
+                const uint16_t sb = ts ? qsv[i] : qsk[i];
                 u4 lo, hi;
-                dequant16(q[b], (_Float16)sc[b], lo, hi);  // sc[b] is an fp16 value: exact
-                unsigned char* row = stage0 + ts * Gm::STAGE_K + r * Gm::ROWB;
-                *reinterpret_cast<u4*>(row + (((2 * c) ^ Gm::swz(r)) * 16)) = lo;
-                *reinterpret_cast<u4*>(row + (((2 * c + 1) ^ Gm::swz(r)) * 16)) = hi;
+                dequant16(q, __builtin_bit_cast(_Float16, sb), lo, hi);
+                unsigned char* row = dst + ts * Gm::STAGE_K + r * Gm::ROWB;
+                *reinterpret_cast<u4*>(row + (((2 * qch) ^ Gm::swz(r)) * 16)) = lo;
+                *reinterpret_cast<u4*>(row + (((2 * qch + 1) ^ Gm::swz(r)) * 16)) = hi;
             }
         }
     };
@@ -627,21 +385,32 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
 
     auto step = [&](int tile, auto stage_tag, auto n_tag) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
-        // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
-        // wave's part of the stage has landed and every wave is done with the other stage
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const unsigned char* sk = Q8 ? stage0 : (decltype(stage_tag)::value ? stage1 : stage0);
-        const unsigned char* sv = sk + Gm::STAGE_K;
-        // the next stage's DMA into the other buffer, in flight during this stage's compute
-        if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - decltype(stage_tag)::value>{});
-        if constexpr (Q8) {
-            // every wave is done with the previous stage's fp16 tile (first barrier)
-            decode(decltype(stage_tag)::value ? stage2 : stage1);
-            __syncthreads();
-        }
+        constexpr int B = decltype(stage_tag)::value;
         const int kpos0 = tile * kP2KS + wrow;  // this wave's first key position
-        compute(n_tag, sk, sv, kpos0);
+        if constexpr (Q8) {
+            // stage `tile` is in fp16 buffer B (decoded by every wave, then a barrier).
+            // After this stage's MFMAs are issued, the wave decodes its share of the next
+            // stage (its own copies, landed during this stage) into the other buffer, which
+            // every wave finished reading before the last barrier, and copies the stage
+            // after it into its raw region; the decode's vector work overlaps the MFMAs.
+            const unsigned char* sk = B ? stage1 : stage0;
+            compute(n_tag, sk, sk + Gm::STAGE_K, kpos0);
+            if (tile + 1 < ntiles) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                decode_q8(B ? stage0 : stage1);
+                if (tile + 2 < ntiles) issue_q8(tile + 2);
+            }
+            __syncthreads();
+        } else {
+            // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
+            // wave's part of the stage has landed and every wave is done with the other stage
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            const unsigned char* sk = B ? stage1 : stage0;
+            // the next stage's DMA into the other buffer, in flight during this stage's compute
+            if (tile + 1 < ntiles) issue(tile + 1, std::integral_constant<int, 1 - B>{});
+            compute(n_tag, sk, sk + Gm::STAGE_K, kpos0);
+        }
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
@@ -650,7 +419,15 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     // both shares' values live and spills when RA != RB)
     using NA = std::integral_constant<int, RA>;
     using NB = std::integral_constant<int, RB>;
-    issue(0, S0{});
+    if constexpr (Q8) {
+        issue_q8(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        decode_q8(stage0);
+        if (ntiles > 1) issue_q8(1);
+        __syncthreads();
+    } else {
+        issue(0, S0{});
+    }
     if (RA == RB || grp == 0) {
         for (int tile = 0; tile < ntiles; tile += 2) {
             step(tile, S0{}, NA{});
@@ -746,26 +523,12 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
     }
 }
 
-template <int D, bool Q8>
-int launch_pf(const PrefillParams& p, hipStream_t stream) {
-    const int R = p.T * p.G;
-    const dim3 grid((R + kPfRowsWG - 1) / kPfRowsWG, p.Hkv);
-    hipLaunchKernelGGL((fa_prefill_kernel<D, Q8>), grid, dim3(kPfThreads), 0, stream, p);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
 
 }  // namespace
 
 int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t stream) {
-    // the int8 DMA copies the scales by dwords: a scale array off 4-byte alignment takes
-    // the register-staged kernel
-    const bool scale_dma = ((reinterpret_cast<uintptr_t>(p.k_scale) | reinterpret_cast<uintptr_t>(p.v_scale)) & 3) == 0;
-    if (head_dim == 128)
-        return !q8 ? launch_dma_rt<128, false>(p, stream)
-                   : scale_dma ? launch_dma_rt<128, true>(p, stream) : launch_pf<128, true>(p, stream);
-    if (head_dim == 64)
-        return !q8 ? launch_dma_rt<64, false>(p, stream)
-                   : scale_dma ? launch_dma_rt<64, true>(p, stream) : launch_pf<64, true>(p, stream);
+    if (head_dim == 128) return !q8 ? launch_dma_rt<128, false>(p, stream) : launch_dma_rt<128, true>(p, stream);
+    if (head_dim == 64) return !q8 ? launch_dma_rt<64, false>(p, stream) : launch_dma_rt<64, true>(p, stream);
     return -2;
 }
 

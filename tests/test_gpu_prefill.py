@@ -81,7 +81,7 @@ def test_config4_chunk_q8(gpu, oracle, p0):
 
 
 def test_q8_scales_off_dword_alignment(gpu, oracle):
-    """Scale arrays 2 bytes off 4-byte alignment take the register-staged kernel; same results."""
+    """Scale arrays 2 bytes off 4-byte alignment (the scales are read as 2-byte values): same results."""
     fa = gpu
     Hq, Hkv, d, T, p0 = 32, 8, 128, 70, 300
     rng = np.random.default_rng(17)
