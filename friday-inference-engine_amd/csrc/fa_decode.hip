@@ -373,6 +373,14 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     constexpr int PPT = ROPE ? HD2 / TPH : 1;     // q rotation pairs per thread (16 head columns x D/2 pairs)
     constexpr int CW = Q8 ? 16 : 8;                       // values of one row chunk
     constexpr int NH = ROPE ? CW / 8 : 1;                 // fp16 vectors of one row chunk
+    // q rotation. Contiguous caches: every lane rotates its own fragment in registers (no LDS,
+    // no barrier) with the RoPE table entries of its own pairs, qcs (NeoX: i = 32 s + 8 kb + j,
+    // s < KSTEPS/2, partner in k-step s + KSTEPS/2 of the same lane; interleaved:
+    // i = 16 s + 4 kb + j, pair (2j, 2j + 1) of k-step s). Paged (a smaller register budget):
+    // the rotation is spread over the workgroup (rq0, rq1, rcs) and read back through LDS.
+    constexpr bool QREG = ROPE && !PAGED;
+    constexpr int NQC = QREG ? D / 8 : 1;
+    float2 qcs[NQC];
     _Float16 rq0[PPT], rq1[PPT];
     float2 rcs[PPT];
     h8 nk[NH], nkp[NH], nv[NH];
@@ -407,7 +415,28 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         if constexpr (!ROPE) return;
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
-        if (rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
+        if (QREG && rot_q) {
+            if (p.neox) {
+#pragma unroll
+                for (int s = 0; s < Gm::KSTEPS / 2; ++s)
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        const f4 c2 = *reinterpret_cast<const f4*>(cs + 32 * s + 8 * kb + j);
+                        qcs[8 * s + j] = float2{c2[0], c2[1]};
+                        qcs[8 * s + j + 1] = float2{c2[2], c2[3]};
+                    }
+            } else {
+#pragma unroll
+                for (int s = 0; s < Gm::KSTEPS; ++s)
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        const f4 c2 = *reinterpret_cast<const f4*>(cs + 16 * s + 4 * kb + j);
+                        qcs[4 * s + j] = float2{c2[0], c2[1]};
+                        qcs[4 * s + j + 1] = float2{c2[2], c2[3]};
+                    }
+            }
+        }
+        if (!QREG && rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
             const int hg = gb * 16 + tid / TPH, i0 = (tid % TPH) * PPT;
             const uint16_t* qr = p.q + ((size_t)b * p.Hq + kvh * p.G + (hg < p.G ? hg : 0)) * D;
 #pragma unroll
@@ -444,7 +473,31 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     float ksc = 0.0f, vsc = 0.0f;
     auto prepare = [&]() __attribute__((always_inline)) {
         if constexpr (ROPE) {
-            if (rot_q) {
+            if (QREG && rot_q) {
+                if (p.neox) {
+                    constexpr int KH = Gm::KSTEPS / 2;
+#pragma unroll
+                    for (int s = 0; s < KH; ++s)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            _Float16 r0, r1;
+                            rope_rotate((float)qf[s][j], (float)qf[s + KH][j], qcs[8 * s + j].x, qcs[8 * s + j].y, r0, r1);
+                            qf[s][j] = r0;
+                            qf[s + KH][j] = r1;
+                        }
+                } else {
+#pragma unroll
+                    for (int s = 0; s < Gm::KSTEPS; ++s)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            _Float16 r0, r1;
+                            rope_rotate((float)qf[s][2 * j], (float)qf[s][2 * j + 1], qcs[4 * s + j].x, qcs[4 * s + j].y, r0, r1);
+                            qf[s][2 * j] = r0;
+                            qf[s][2 * j + 1] = r1;
+                        }
+                }
+            }
+            if (!QREG && rot_q) {
                 // The rotation of the group's q rows is spread over the workgroup (thread t:
                 // rotation pairs i0 .. i0 + PPT - 1 of head column t / TPH, from the values
                 // load_inputs fetched), and every lane reads its rotated fragment back from LDS.
