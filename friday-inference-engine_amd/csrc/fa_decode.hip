@@ -69,7 +69,9 @@ struct Geo {
     static constexpr int TILES = W * WAVE_LDS;
     static constexpr int COMB_OFF = ALIAS ? 0 : TILES;
     static constexpr int QX_OFF = ALIAS ? (TILES > COMB_LDS ? TILES : COMB_LDS) : TILES + COMB_LDS;  // rotated q rows
-    static constexpr int LDS = QX_OFF + 16 * D * 2;  // tiles, the wave combine, the q rows (16 heads x D fp16)
+    // tiles, the wave combine, and (paged: the q rotation goes through LDS) the q rows,
+    // 16 heads x D fp16
+    static constexpr int LDS = QX_OFF + (ALIAS ? 16 * D * 2 : 0);
     // LDS slot of the 16-byte chunk k (values 8k .. 8k+7) of a tile row. int8 rows: lane c
     // dequantises chunks 2c and 2c+1 and writes them with two instructions; placing even
     // chunks in slots 0 .. D/16-1 and odd ones after them makes each instruction's lanes of
@@ -415,7 +417,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         if constexpr (!ROPE) return;
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
-        if (QREG && rot_q) {
+        if constexpr (QREG) if (rot_q) {
             if (p.neox) {
 #pragma unroll
                 for (int s = 0; s < Gm::KSTEPS / 2; ++s)
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
                     }
             }
         }
-        if (!QREG && rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
+        if constexpr (!QREG) if (rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
             const int hg = gb * 16 + tid / TPH, i0 = (tid % TPH) * PPT;
             const uint16_t* qr = p.q + ((size_t)b * p.Hq + kvh * p.G + (hg < p.G ? hg : 0)) * D;
 #pragma unroll
@@ -473,7 +475,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     float ksc = 0.0f, vsc = 0.0f;
     auto prepare = [&]() __attribute__((always_inline)) {
         if constexpr (ROPE) {
-            if (QREG && rot_q) {
+            if constexpr (QREG) if (rot_q) {
                 if (p.neox) {
                     constexpr int KH = Gm::KSTEPS / 2;
 #pragma unroll
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
                         }
                 }
             }
-            if (!QREG && rot_q) {
+            if constexpr (!QREG) if (rot_q) {
                 // The rotation of the group's q rows is spread over the workgroup (thread t:
                 // rotation pairs i0 .. i0 + PPT - 1 of head column t / TPH, from the values
                 // load_inputs fetched), and every lane reads its rotated fragment back from LDS.
