@@ -46,7 +46,7 @@ MALL_BYTES = 256 << 20         # Infinity Cache: a "cold" working set must excee
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs recorded in the profile below (KiB per
 # dispatch, scaled by the copy-kernel calibration FETCH_SIZE x 2.0, WRITE_SIZE x 1.0);
 # it is not measured in this run.
-HEADLINE_TRAFFIC_BYTES = 135853839
+HEADLINE_TRAFFIC_BYTES = 135877734
 TRAFFIC_SOURCE = "constant from profiles/decode_step_cfg3_pmc.txt (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)"
 
 
