@@ -115,11 +115,18 @@ __device__ __forceinline__ float wave_max_xor(float v, int mask) { return fmaxf(
 
 // max of v over the lanes l, l^16, l^32, l^48 (the four lane blocks of an MFMA
 // column) with the gfx950 VALU lane swaps, no LDS round trip
+// v_max_f32 as the hardware does it: a quiet NaN operand yields the other operand. (fmaxf
+// on values that come out of a lane swap first quiets each operand with a v_max of itself.)
+__device__ __forceinline__ float max_raw(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float col_max4(float v) {
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    v = max_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float wave_sum_xor(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
 

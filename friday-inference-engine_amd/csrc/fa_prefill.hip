@@ -345,10 +345,23 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             h8 pf[N];
 #pragma unroll
             for (int rt = 0; rt < N; ++rt) {
-                const float nb = kNegBig - m_run[rt];
+                if constexpr (BF) {
+                    const float nb = kNegBig - m_run[rt];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    pf[rt][j] = to_p<BF>(exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), nb)));
+                    for (int j = 0; j < 8; ++j)
+                        pf[rt][j] = to_p<BF>(exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), nb)));
+                } else {
+                    // the same rule on the fp16 weights, two per instruction: a NaN weight (and
+                    // only a NaN, all others are >= 0) becomes w, the weight of a score of -1e30:
+                    // 1 while m_run is -1e30, else 0 (exp2(-1e30 - m_run) rounds to 0)
+                    const uint32_t w = m_run[rt] == kNegBig ? 0x3C003C00u : 0u;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) pf[rt][j] = (_Float16)exp2_fast(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]));
+                    u4 pb = *reinterpret_cast<const u4*>(&pf[rt]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) asm("v_pk_max_f16 %0, %1, %2" : "=v"(pb[i]) : "v"(pb[i]), "v"(w));
+                    pf[rt] = *reinterpret_cast<const h8*>(&pb);
+                }
             }
             if (!full) {
 #pragma unroll
