@@ -44,9 +44,11 @@ constexpr int kP2Slices = 4;                // key slices of a stage (one wave e
 constexpr int kP2Groups = 2;                // row-tile groups sharing every stage
 constexpr int kP2Waves = kP2Slices * kP2Groups;
 constexpr int kP2Threads = kP2Waves * 64;
-// Group 0 issues every stage copy: it starts a stage behind group 1, whose QK MFMAs and
-// softmax then overlap group 0's copy issue, which waits on the memory pipeline.
-constexpr int kP2DmaWaves = kP2Slices;
+// Every wave issues an equal share of each stage copy, all of its K rows before its V rows.
+// (Measured at config 4, p0 = 7680: 111.7-111.9 us; group 0 issuing all copies with K and
+// V interleaved per instruction 117.8-119.0 us, K before V 115.0-115.9 us; group 0 the K
+// part and group 1 the V part 113.0-113.7 us.)
+constexpr int kP2DmaWaves = kP2Waves;
 constexpr int kP2KW = 32;                   // keys per wave per stage
 constexpr int kP2KS = kP2KW * kP2Slices;    // keys per stage (128)
 constexpr float kLazy = 8.0f;               // log2 slack of the reference max (weights <= 256)
@@ -172,46 +174,33 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     // first token of the group's first tile: slices up to it need no causal mask
     const int grp_lo = row0 < R ? p0 + row0 / p.G : INT_MAX;
 
-    // fp16 stage copy: wave w < kP2DmaWaves moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K and
-    // V parts, each 16-byte chunk to its swizzled slot
+    // fp16 stage copy: wave w moves rows [w*NI*RPI, (w+1)*NI*RPI) of the K part, then the same
+    // rows of the V part, each 16-byte chunk to its swizzled slot
     constexpr int CROWB = Q8 ? Rg::ROWB : Gm::ROWB;  // cache bytes of one kv-head row
     const size_t rowb = (size_t)p.Hkv * CROWB;
     const char* kbase = static_cast<const char*>(p.k) + (size_t)kvh * CROWB;
     const char* vbase = static_cast<const char*>(p.v) + (size_t)kvh * CROWB;
     const int drow = lane / Gm::CPR, dslot = lane % Gm::CPR;
-    uint32_t doff[Gm::NI];
-#pragma unroll
-    for (int i = 0; i < Gm::NI; ++i) {
-        const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
-        doff[i] = (uint32_t)(r * (int)rowb + (dslot ^ Gm::swz(r)) * 16);
-    }
     lds_u8* const lds0 = (lds_u8*)stage0;
     lds_u8* const lds1 = (lds_u8*)stage1;
     auto issue = [&](int tile, auto stage_tag) __attribute__((always_inline)) {
-        if (wave >= kP2DmaWaves) return;
         lds_u8* st = decltype(stage_tag)::value ? lds1 : lds0;
         // uniform base: the tile's first key
         const size_t tile0 = (size_t)tile * kP2KS * rowb;
         const char* kt = kbase + tile0;
         const char* vt = vbase + tile0;
         const int rmax = kend - 1 - tile * kP2KS;  // rows past it re-read the last key
-        if (rmax >= kP2KS - 1) {
+        // (one form for every stage: a separate unclamped form for full stages, chosen by a
+        // branch, measured 7 % slower at config 4, p0 = 7680)
+        uint32_t off[Gm::NI];
 #pragma unroll
-            for (int i = 0; i < Gm::NI; ++i) {
-                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
-                dma16(kt, doff[i], l);
-                dma16(vt, doff[i], l + Gm::STAGE_K);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < Gm::NI; ++i) {
-                const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
-                const uint32_t off = (uint32_t)(min(r, rmax) * (int)rowb + (dslot ^ Gm::swz(r)) * 16);
-                lds_u8* l = st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB;
-                dma16(kt, off, l);
-                dma16(vt, off, l + Gm::STAGE_K);
-            }
+        for (int i = 0; i < Gm::NI; ++i) {
+            const int r = (wave * Gm::NI + i) * Gm::RPI + drow;
+            off[i] = (uint32_t)(min(r, rmax) * (int)rowb + (dslot ^ Gm::swz(r)) * 16);
+            dma16(kt, off[i], st + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB);
         }
+#pragma unroll
+        for (int i = 0; i < Gm::NI; ++i) dma16(vt, off[i], st + Gm::STAGE_K + (wave * Gm::NI + i) * Gm::RPI * Gm::ROWB);
     };
     // int8 stage copy: every wave moves its own rows [w*WROWS, (w+1)*WROWS) of K and V into
     // its raw region (lane l's 16 codes at + 16 l of each instruction) and loads the fp16
