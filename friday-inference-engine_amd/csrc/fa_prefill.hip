@@ -44,10 +44,10 @@ constexpr int kP2Slices = 4;                // key slices of a stage (one wave e
 constexpr int kP2Groups = 2;                // row-tile groups sharing every stage
 constexpr int kP2Waves = kP2Slices * kP2Groups;
 constexpr int kP2Threads = kP2Waves * 64;
-// Every wave issues an equal share of each stage copy, all of its K rows before its V rows.
-// (Measured at config 4, p0 = 7680: 111.7-111.9 us; group 0 issuing all copies with K and
-// V interleaved per instruction 117.8-119.0 us, K before V 115.0-115.9 us; group 0 the K
-// part and group 1 the V part 113.0-113.7 us.)
+// Every wave issues an equal share of each stage copy: its K rows right after the stage's
+// barrier, its V rows once the wave's S^T MFMAs of the stage are issued. (Measured at
+// config 4, p0 = 7680: 109.6-110.4 us; both parts at the barrier 111.7-111.9 us; group 0
+// issuing all copies with K and V interleaved per instruction 117.8-119.0 us.)
 constexpr int kP2DmaWaves = kP2Waves;
 constexpr int kP2KW = 32;                   // keys per wave per stage
 constexpr int kP2KS = kP2KW * kP2Slices;    // keys per stage (128)
