@@ -113,6 +113,28 @@ def test_config4_chunk(gpu, oracle, p0):
         assert_close(got[t], ref, f"config4 p0={p0} t={t}")
 
 
+# T for each row-tile share the launcher picks at 32q/8kv (ceil(T * 4 * 8 / 4096) tiles per
+# workgroup): (1,0), (1,1), (2,1), (2,2), (3,2), (3,3)
+SHARE_T = [100, 200, 300, 500, 600, 700]
+
+
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("T", SHARE_T)
+def test_every_row_share(gpu, oracle, T, q8):
+    """Every row-tile share of the workgroup (which sets how the waves split the stage copies,
+    including a group without rows) on a ragged prefix; sampled rows vs the decode oracle."""
+    fa = gpu
+    Hq, Hkv, d, p0 = 32, 8, 128, 37
+    rng = np.random.default_rng(900 + T + q8)
+    q = f16(rng, (T, Hq * d))
+    k, v, ks, vs = make_cache(rng, p0 + T, Hkv * d, q8)
+    got = run_prefill(fa, q, k, v, ks, vs, T, p0, Hq, Hkv, d)
+    for t in sorted(set([0, 1, 90, T // 2, T - 2, T - 1] + list(rng.choice(T, 4, replace=False)))):
+        S = p0 + t + 1
+        ref = oracle.decode_q8(q[t], k, ks, v, vs, S, Hq, Hkv, d) if q8 else oracle.decode(q[t], k, v, S, Hq, Hkv, d)
+        assert_close(got[t], ref, f"share T={T} q8={q8} t={t}")
+
+
 @pytest.mark.parametrize("Hq,Hkv,d,T,p0,q8", [(10, 2, 128, 77, 100000, False), (10, 2, 128, 77, 60000, True),
                                                (14, 2, 64, 200, 30000, False),
                                                (10, 2, 128, 2048, 100, False), (10, 2, 128, 2047, 9, True)])
