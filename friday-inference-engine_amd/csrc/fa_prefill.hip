@@ -348,9 +348,13 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
                     for (int j = 0; j < 8; ++j)
                         pf[rt][j] = to_p<BF>(exp2_fast(fmaxf(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]), nb)));
                 } else {
-                    // the same rule on the fp16 weights, two per instruction: a NaN weight (and
-                    // only a NaN, all others are >= 0) becomes w, the weight of a score of -1e30:
-                    // 1 while m_run is -1e30, else 0 (exp2(-1e30 - m_run) rounds to 0)
+                    // the same rule on the fp16 weights, two per instruction: max(weight, w) with
+                    // w the weight of a score of -1e30 (1 while m_run is -1e30, else 0, as
+                    // exp2(-1e30 - m_run) rounds to 0) turns a NaN weight into w and keeps every
+                    // other weight (>= 0) when w = 0. While m_run is -1e30 no finite score has been
+                    // seen (it would have moved m_run), so the other weights then are those of
+                    // masked keys, zeroed below, and of -inf scores, which the fp32 form also
+                    // clamped to weight 1.
                     const uint32_t w = m_run[rt] == kNegBig ? 0x3C003C00u : 0u;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) pf[rt][j] = (_Float16)exp2_fast(__builtin_fmaf(x[rt][j], p.scale2, -m_run[rt]));
