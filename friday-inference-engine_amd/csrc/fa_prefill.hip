@@ -93,9 +93,10 @@ struct P2RawGeo {
 // Issued from inline assembly: the compiler would otherwise drain every such copy before
 // any later LDS read, including reads of the other stage buffer; the kernel waits for
 // the copies itself (s_waitcnt vmcnt(0) + barrier) before reading the stage they fill.
+// Non-temporal (nt): measured 2 % faster on int8 caches and at p0 = 0, the same elsewhere.
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 __device__ __forceinline__ void dma16(const char* base, uint32_t off, lds_u8* lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"((uint32_t)(size_t)lds), "v"(off), "s"(base)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"((uint32_t)(size_t)lds), "v"(off), "s"(base)
                  : "memory");
 }
 
