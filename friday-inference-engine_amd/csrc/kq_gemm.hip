@@ -616,8 +616,15 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
 // LDS at the same offsets mod 4 as in memory, so the 2-byte aligned kinds use the same
 // realigning loads.
 typedef __attribute__((address_space(3))) unsigned char gv_lds_u8;
+// The GEMV's copies (the weight rows, each read once per call, and the activations) are
+// non-temporal (nt): measured 4-5 % faster on the 32B attn_output and 8B ffn_down shapes
+// than the default policy.
+__device__ __forceinline__ void dma16_nt(const void* base, uint32_t off, gv_lds_u8* lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds_sgpr((const void*)lds)), "v"(off), "s"(base)
+                 : "memory");
+}
 __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, gv_lds_u8* lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_sgpr((const void*)lds)), "v"(off),
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2 nt" ::"s"(lds_sgpr((const void*)lds)), "v"(off),
                  "s"(base)
                  : "memory");
 }
@@ -661,7 +668,7 @@ __device__ __forceinline__ float gemv_row(const unsigned char* wrow, const int8_
 // span rounded up to 256 bytes.
 __device__ __forceinline__ void copy_span(const void* src, uint32_t span, gv_lds_u8* lds, int wave, int nw, int lane) {
     const uint32_t big = (reinterpret_cast<uintptr_t>(src) & 15) == 0 ? span / 1024 : 0;
-    for (uint32_t i = wave; i < big; i += nw) gm_dma16(src, 1024 * i + 16 * lane, lds + 1024 * i);
+    for (uint32_t i = wave; i < big; i += nw) dma16_nt(src, 1024 * i + 16 * lane, lds + 1024 * i);
     const uint32_t rest0 = 1024 * big;
     const uint32_t pieces = (span - rest0 + 255) / 256;
     for (uint32_t i = wave; i < pieces; i += nw)
