@@ -33,15 +33,16 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
     // element offsets of the chunk (and, NeoX, its partner chunk)
     const int e0 = 8 * c, e1 = p.neox ? hd2 + 8 * c : 8 * c;
     // the loads whose addresses do not depend on the position go out before it is read, so
-    // their latency overlaps the position's round trip
-    const h8 a = *reinterpret_cast<const h8*>(x + e0);
-    const h8 bv = *reinterpret_cast<const h8*>(x + e1);
+    // their latency overlaps the position's round trip; they are non-temporal (each value is
+    // read once: T = 512 at 40q/8kv d128 measured 5.5 against 6.3 us with the default policy)
+    const h8 a = __builtin_nontemporal_load(reinterpret_cast<const h8*>(x + e0));
+    const h8 bv = __builtin_nontemporal_load(reinterpret_cast<const h8*>(x + e1));
     const bool store_kv = is_k && p.k_dst;
     const _Float16* vs = reinterpret_cast<const _Float16*>(p.v) + (size_t)t * kv_dim + (h - p.Hq) * p.D;
     h8 v0 = h8{0, 0, 0, 0, 0, 0, 0, 0}, v1 = v0;
     if (store_kv) {
-        v0 = *reinterpret_cast<const h8*>(vs + e0);
-        if (p.neox) v1 = *reinterpret_cast<const h8*>(vs + e1);
+        v0 = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vs + e0));
+        if (p.neox) v1 = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vs + e1));
     }
     const int pos = PAGED ? p.seq_lens[t] - 1 : (p.d_pos ? *p.d_pos : p.pos) + t;
     if (pos < 0 || pos >= p.max_ctx) return;
