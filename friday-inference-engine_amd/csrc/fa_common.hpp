@@ -176,15 +176,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
                                              0x00020000);
 }
 
-// Nontemporal buffer loads (cache policy nt): 16 bytes, and one fp16 value as its bits.
-// Offsets at or past the descriptor's byte count read as zero.
+// Buffer loads; offsets at or past the descriptor's byte count read as zero. 16 bytes with
+// the nontemporal cache policy (nt: K/V rows, read once), and one fp16 value as its bits
+// with the default policy (int8 block scales: one cache line holds every kv head's scales of
+// a position, read by all their workgroups; nt there measured 1 % slower).
 constexpr int kCpolNt = 2;
 __device__ __forceinline__ u4 ld_buf_nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     const i4v x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kCpolNt);
     return *reinterpret_cast<const u4*>(&x);
 }
 __device__ __forceinline__ short ld_buf_f16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, kCpolNt);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, 0);
 }
 // Copies of loaded registers, made at this point of the program into registers other than
 // the source (early clobber). A pipeline stage that is copied out and then reloaded in
