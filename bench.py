@@ -79,29 +79,41 @@ class Ctx:
         consecutive replays) and return (ms per replay, {median, p10, p90} in ms)."""
         fa = self.fa
         graph = fa.Graph(self.stream, fn)
-        for _ in range(warmup):
-            graph.launch()
-        self.stream.synchronize()
-        t0, t1 = fa.Event(), fa.Event()
-        t0.record(self.stream.s)
-        for _ in range(steps):
-            graph.launch()
-        t1.record(self.stream.s)
-        self.stream.synchronize()
-        ms = t0.elapsed_ms(t1) / steps if steps else 0.0
-        if not stats:
-            return ms
-        import numpy as np
+        ev = []
+        try:
+            for _ in range(warmup):
+                graph.launch()
+            self.stream.synchronize()
+            t0, t1 = fa.Event(), fa.Event()
+            ev += [t0, t1]
+            t0.record(self.stream.s)
+            for _ in range(steps):
+                graph.launch()
+            t1.record(self.stream.s)
+            self.stream.synchronize()
+            ms = t0.elapsed_ms(t1) / steps if steps else 0.0
+            if not stats:
+                return ms
+            import numpy as np
 
-        ev = [fa.Event() for _ in range(stats + 1)]
-        ev[0].record(self.stream.s)
-        for i in range(stats):
-            graph.launch()
-            ev[i + 1].record(self.stream.s)
-        self.stream.synchronize()
-        d = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(stats)])
-        return ms, {"replays": stats, "median_ms": round(float(np.median(d)), 4),
-                    "p10_ms": round(float(np.percentile(d, 10)), 4), "p90_ms": round(float(np.percentile(d, 90)), 4)}
+            se = [fa.Event() for _ in range(stats + 1)]
+            ev += se
+            se[0].record(self.stream.s)
+            for i in range(stats):
+                graph.launch()
+                se[i + 1].record(self.stream.s)
+            self.stream.synchronize()
+            d = np.array([se[i].elapsed_ms(se[i + 1]) for i in range(stats)])
+            return ms, {"replays": stats, "median_ms": round(float(np.median(d)), 4),
+                        "p10_ms": round(float(np.percentile(d, 10)), 4),
+                        "p90_ms": round(float(np.percentile(d, 90)), 4)}
+        finally:
+            # the graph holds raw pointers into the caller's buffers, which are freed after
+            # this returns: it must be gone first (and its launches complete)
+            self.stream.synchronize()
+            graph.destroy()
+            for e in ev:
+                e.destroy()
 
 
 class DecodeLayers:

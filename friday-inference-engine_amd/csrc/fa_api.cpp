@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -114,11 +115,24 @@ int max_splits() {
     static const int v = env_int("FRIDAY_ATTN_MAX_SPLITS", kMaxSplitsLimit, 1, kMaxSplitsLimit);
     return v;
 }
+// Compute units of the current device (256 on an MI355X), asked once per device.
+int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 // Splits per (kv head, head block) so that one sequence keeps about `target`
-// workgroups streaming: one per CU of the MI355X (256). The partition stays a
-// function of S and the head layout only, never of the batch.
+// workgroups streaming: one per CU of the device (FRIDAY_ATTN_TARGET_WGS overrides it).
+// The partition stays a function of S, the head layout and the device, never of the batch.
 int splits_for(int Hkv, int ngb) {
-    static const int target = env_int("FRIDAY_ATTN_TARGET_WGS", 256, 1, 1 << 16);
+    static const int target_env = env_int("FRIDAY_ATTN_TARGET_WGS", 0, 0, 1 << 16);
+    const int target = target_env > 0 ? target_env : device_cus();
     const int groups = Hkv * ngb;
     int ns = target / (groups > 0 ? groups : 1);
     ns = ns < 1 ? 1 : ns;
@@ -207,6 +221,8 @@ static int decode_common(const char* w, const uint16_t* q, const void* k, const 
         return fail(FA_ERR_INVALID, "%s: seq_len %d outside [1, %d]", w, seq_len, max_seq);
     const bool q8 = ks && vs;
     if ((ks == nullptr) != (vs == nullptr)) return fail(FA_ERR_INVALID, "%s: give both k_scale and v_scale", w);
+    if (!aligned16(q, k, v, nullptr, nullptr) || reinterpret_cast<uintptr_t>(out) % 8)
+        return fail(FA_ERR_INVALID, "%s: q and the caches must be 16-byte aligned, out 8-byte aligned", w);
     const int G = Hq / Hkv;
     fa::DecodeParams p{};
     p.q = q; p.k = k; p.v = v; p.k_scale = ks; p.v_scale = vs; p.d_pos = d_pos;
@@ -269,6 +285,23 @@ int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, v
                          "decode_workspace_init");
 }
 
+int friday_attn_decode_workspace_status(const void* workspace, size_t workspace_bytes, void* stream) {
+    const char* w = "decode_workspace_status";
+    if (!workspace || workspace_bytes < (fa::kStatusWord + 1) * sizeof(unsigned))
+        return fail(FA_ERR_INVALID, "%s: invalid workspace", w);
+    unsigned word = 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (hipMemcpyAsync(&word, static_cast<const unsigned*>(workspace) + fa::kStatusWord, sizeof(word),
+                       hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return fail(FA_ERR_LAUNCH, "%s: copy failed: %s", w, hipGetErrorString(hipGetLastError()));
+    if (word & fa::kStatusMergeTimeout)
+        return fail(FA_ERR_TIMEOUT,
+                    "%s: a fused merge gave up waiting for its splits; outputs since the last "
+                    "friday_attn_decode_workspace_init are not valid: initialise the workspace again", w);
+    return ok();
+}
+
 int friday_attn_decode_attention_fused(const uint16_t* q, const void* k_cache, const void* v_cache, uint16_t* out,
                                        int seq_len, const int* d_pos, int max_seq_len, int num_heads,
                                        int num_kv_heads, int head_dim, void* workspace, size_t workspace_bytes,
@@ -289,6 +322,9 @@ int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint
         return fail(FA_ERR_INVALID, "%s: invalid arguments", w);
     if (!d_pos && (pos < 0 || pos >= max_ctx))
         return fail(FA_ERR_INVALID, "%s: position %d outside [0, %d)", w, pos, max_ctx);
+    // q, the new k / v rows and the cache rows move as 16-byte chunks, out as 8-byte ones
+    if (!aligned16(q, k, v, k_layer, v_layer) || reinterpret_cast<uintptr_t>(out) % 8)
+        return fail(FA_ERR_INVALID, "%s: q, k, v and the caches must be 16-byte aligned, out 8-byte aligned", w);
     const bool q8 = k_scale != nullptr;
     const int G = num_heads / num_kv_heads;
     fa::DecodeParams p{};
@@ -337,30 +373,25 @@ constexpr size_t kScratchBytes = size_t(4) << 20;
 constexpr size_t kScratchCounterBytes = size_t(1) << 20;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-struct ScratchSlot {
-    std::once_flag once;
-    void* ptr = nullptr;
-    hipError_t err = hipSuccess;
-};
-ScratchSlot g_scratch[64];
-
 // The device address of the current device's scratch (the host-side name `scratch` is not
-// one), looked up once per device; the first call also zeroes it with a fill kernel on
-// `stream` (counter and base start equal; every completed call advances both by the same
-// amount, so they stay consistent).
-void* scratch_ptr(hipStream_t stream, hipError_t* err) {
+// one), looked up once per device with that device current and kept. Nothing is launched:
+// the array is zero when the code object is loaded (counter and base start equal, and every
+// completed call advances both by the same amount), so the first call may be made under
+// stream capture or on any stream. A failed lookup is not kept; the next call tries again.
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+void* scratch_ptr(hipError_t* err) {
     int dev = 0;
     if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
     if (dev < 0 || dev >= 64) return *err = hipErrorInvalidDevice, nullptr;
-    ScratchSlot& s = g_scratch[dev];
-    std::call_once(s.once, [&] {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
         void* ptr = nullptr;
-        s.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (s.err == hipSuccess && fa::launch_zero_fill(ptr, kScratchBytes, stream) != 0) s.err = hipGetLastError();
-        if (s.err == hipSuccess) s.ptr = ptr;
-    });
-    *err = s.err;
-    return s.ptr;
+        if ((*err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess) return nullptr;
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
 }
 }  // namespace
 
@@ -379,8 +410,10 @@ int friday_attn_decode_step_noalloc(uint16_t* q, const uint16_t* k, const uint16
     if (counters_bytes(1, num_heads) > kScratchCounterBytes || need > kScratchBytes)
         return fail(FA_ERR_WORKSPACE, "%s: needs %zu bytes of scratch, more than the %zu held per GPU", w, need,
                     kScratchBytes);
+    if (!aligned16(q, k, v, k_layer, v_layer) || reinterpret_cast<uintptr_t>(out) % 8)
+        return fail(FA_ERR_INVALID, "%s: q, k, v and the caches must be 16-byte aligned, out 8-byte aligned", w);
     hipError_t err = hipSuccess;
-    void* ws = scratch_ptr(static_cast<hipStream_t>(stream), &err);
+    void* ws = scratch_ptr(&err);
     if (!ws) return fail(FA_ERR_LAUNCH, "%s: device scratch unavailable: %s", w, hipGetErrorString(err));
     return decode_step_common(w, q, k, v, k_layer, v_layer, nullptr, nullptr, out, d_pos, pos, max_ctx, num_heads,
                               num_kv_heads, head_dim, rope_table, neox, ws, kScratchBytes, stream, nullptr, nullptr,
@@ -460,6 +493,8 @@ static int paged_decode_common(const char* w, uint16_t* q, const uint16_t* k_new
     if (block_table_stride <= 0 || (long long)block_table_stride * FA_PAGE_TOKENS < max_seq_len)
         return fail(FA_ERR_INVALID, "%s: block_table_stride %d cannot address max_seq_len %d", w,
                     block_table_stride, max_seq_len);
+    if (!aligned16(q, k_new, v_new, k_pool, v_pool) || reinterpret_cast<uintptr_t>(out) % 8)
+        return fail(FA_ERR_INVALID, "%s: q, k, v and the pools must be 16-byte aligned, out 8-byte aligned", w);
     const int G = num_heads / num_kv_heads;
     fa::DecodeParams p{};
     p.q = q; p.k = k_pool; p.v = v_pool; p.block_table = block_table; p.bt_stride = block_table_stride;

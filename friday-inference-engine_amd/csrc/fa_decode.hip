@@ -47,7 +47,6 @@ constexpr int kShortStages = 4;  // stages when a wave has at most this many til
 constexpr int kPagedWgsPerCu = 3;
 constexpr int kShortStagesPaged = 2;
 constexpr int kMergeSlices = 8;  // column slices of the distributed fused merge
-constexpr size_t kCus = 256;  // compute units of an MI355X
 constexpr float kLazy2 = 8.0f;   // lazy softmax reference: rescale when a max rises by > 2^8
 
 // ALIAS: the wave combine reuses the tile region (after a barrier), so that two workgroups
@@ -285,14 +284,16 @@ __device__ __forceinline__ int merge_slices(const DecodeParams& p, int nsp) {
 
 // Wait of one thread until the arrival counter reaches `target` (unsigned, wrapping). The
 // workgroups it waits for were dispatched before the waiting one, so the wait ends; it is
-// still bounded (kSpinTicks of the 100 MHz real-time clock), after which the merge goes
-// ahead with whatever partials are there.
+// still bounded (kSpinTicks of the 100 MHz real-time clock) so that a broken dispatch
+// assumption cannot hang the GPU. Returns false when it gave up: the caller then records
+// the failure in the workspace's sticky error word and does not merge.
 constexpr uint64_t kSpinTicks = 100000000;  // 1 s
-__device__ __forceinline__ void wait_count(const unsigned* cnt, unsigned target) {
+__device__ __forceinline__ bool wait_count(const unsigned* cnt, unsigned target) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while ((int)(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) return;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) return false;
     }
+    return true;
 }
 
 // Workgroups per CU the register budget is set for: fp16 two (two waves per SIMD, up to 256
@@ -911,8 +912,17 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         }
         if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (mk < 0) return;
-        if (tid == 0) wait_count(cnt, base + (unsigned)nsp);
+        // a merger that gives up waiting sets the workspace's sticky error bit (a vector
+        // atomic) and merges nothing: neither the output, nor q, nor the base is written
+        __shared__ int gave_up;
+        if (tid == 0) {
+            gave_up = !wait_count(cnt, base + (unsigned)nsp);
+            if (gave_up)
+                __hip_atomic_fetch_or(reinterpret_cast<unsigned*>(p.counters) + kStatusWord, kStatusMergeTimeout,
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         __syncthreads();
+        if (gave_up) return;
         merge_slice<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
         if (mk == 0) {
             write_q();  // every workgroup of the group has read q by now
@@ -937,7 +947,7 @@ int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
     // fixed mergers while the whole grid can be resident at once, else the last arriver merges
-    const size_t resident = kCus * wgs_per_cu(PAGED, Q8);
+    const size_t resident = (size_t)device_cus() * wgs_per_cu(PAGED, Q8);
     p.merge_slices = (size_t)grid.x * grid.y * grid.z <= resident ? kMergeSlices : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages

@@ -20,6 +20,12 @@ constexpr int kMaxSplitsLimit = 128;
 // arrival counters of the fused merge sit 256 bytes apart, so that the atomics of
 // different head groups do not queue on one cache line
 constexpr int kCounterStride = 64;
+// Sticky error word of a decode workspace: int index kStatusWord of counter slot 0 (byte 192,
+// away from slot 0's counter at 0 and base at 128). A fused merge that gives up waiting for
+// its arrival count sets bit kStatusMergeTimeout there; friday_attn_decode_workspace_status
+// reports it and friday_attn_decode_workspace_init clears it.
+constexpr int kStatusWord = 48;
+constexpr unsigned kStatusMergeTimeout = 1u;
 
 __host__ __device__ inline int split_bound(int S, int min_chunk, int max_splits) {
     int ns = S > 0 ? (S + min_chunk - 1) / min_chunk : 1;
@@ -41,6 +47,7 @@ __host__ __device__ inline int split_count(int S, int min_chunk, int max_splits)
 int min_chunk();
 int max_splits();
 int splits_for(int Hkv, int ngb);
+int device_cus();  // compute units of the current device
 
 struct DecodeParams {
     const uint16_t* q;         // [B][Hq*D]

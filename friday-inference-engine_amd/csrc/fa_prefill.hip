@@ -532,7 +532,8 @@ int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
         return e && *e ? std::atoi(e) : 0;
     }();
     const long rows = (long)p.T * p.G * p.Hkv;
-    int rt = forced > 0 ? forced : (int)((rows + 256 * 16 - 1) / (256 * 16));
+    const size_t cu16 = (size_t)device_cus() * 16;  // one row tile per CU and wave group
+    int rt = forced > 0 ? forced : (int)((rows + cu16 - 1) / cu16);
     const int rt_max = 6;
     rt = rt < 1 ? 1 : (rt > rt_max ? rt_max : rt);
     switch (rt) {

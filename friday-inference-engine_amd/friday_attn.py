@@ -26,6 +26,7 @@ FA_ERR_INVALID = -1
 FA_ERR_UNSUPPORTED = -2
 FA_ERR_LAUNCH = -3
 FA_ERR_WORKSPACE = -4
+FA_ERR_TIMEOUT = -5
 PAGE_TOKENS = 16
 
 # (name, restype, argtypes) of every C-ABI entry point in include/friday_attn.h
@@ -44,6 +45,7 @@ API = [
     ("friday_attn_split_workspace_bytes", _SZ, [_I, _I]),
     ("friday_attn_decode_attention_split", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     ("friday_attn_decode_workspace_init", _I, [_P, _SZ, _P]),
+    ("friday_attn_decode_workspace_status", _I, [_P, _SZ, _P]),
     ("friday_attn_decode_attention_fused", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     ("friday_attn_decode_step", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_decode_step_noalloc", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
@@ -163,7 +165,7 @@ class Hip:
 
 
 class Stream:
-    """A default-priority HIP stream."""
+    """A default-priority HIP stream, destroyed by destroy() or when collected."""
 
     def __init__(self):
         s = C.c_void_p()
@@ -173,36 +175,100 @@ class Stream:
     def synchronize(self):
         Hip.check(Hip.lib().hipStreamSynchronize(self.s), "hipStreamSynchronize")
 
+    def destroy(self):
+        if self.s:
+            s, self.s = self.s, None
+            Hip.check(Hip.lib().hipStreamDestroy(s), "hipStreamDestroy")
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+# Graphs that are instantiated and not yet destroyed. A graph's kernel nodes hold the raw
+# device pointers of every buffer that was alive while it was captured; freeing one of
+# those buffers while the graph lives would leave the graph pointing at memory that the
+# next allocation reuses, so DeviceBuffer.free() refuses it.
+_live_graphs: dict = {}
+
 
 class Graph:
-    """Capture of the launches issued on `stream` by fn(), replayed with launch()."""
+    """Capture of the launches issued on `stream` by fn(), replayed with launch().
+
+    destroy() (or leaving a `with` block) releases the executable graph and the graph:
+    do that before freeing any buffer the captured launches use."""
 
     def __init__(self, stream: Stream, fn):
         h = Hip.lib()
+        self.exec = self.graph = None
         Hip.check(h.hipStreamBeginCapture(stream.s, 2), "hipStreamBeginCapture")  # relaxed mode
         try:
             fn()
         finally:
             g = C.c_void_p()
-            Hip.check(h.hipStreamEndCapture(stream.s, C.byref(g)), "hipStreamEndCapture")
+            rc = h.hipStreamEndCapture(stream.s, C.byref(g))
+        Hip.check(rc, "hipStreamEndCapture")
         self.graph = g.value
         e = C.c_void_p()
-        Hip.check(h.hipGraphInstantiate(C.byref(e), self.graph, None, None, 0), "hipGraphInstantiate")
+        try:
+            Hip.check(h.hipGraphInstantiate(C.byref(e), self.graph, None, None, 0), "hipGraphInstantiate")
+        except Exception:
+            h.hipGraphDestroy(self.graph)
+            self.graph = None
+            raise
         self.exec = e.value
         self.stream = stream
+        self.captured = frozenset(DeviceBuffer._live)  # buffers the launches may reference
+        _live_graphs[id(self)] = self
 
     def launch(self):
+        if not self.exec:
+            raise RuntimeError("Graph.launch after destroy()")
         Hip.check(Hip.lib().hipGraphLaunch(self.exec, self.stream.s), "hipGraphLaunch")
+
+    def destroy(self):
+        """Release the executable graph, then the graph (a launch in flight completes first:
+        HIP defers the release of an executable graph until its launches are done)."""
+        h = Hip.lib()
+        _live_graphs.pop(id(self), None)
+        if self.exec:
+            e, self.exec = self.exec, None
+            Hip.check(h.hipGraphExecDestroy(e), "hipGraphExecDestroy")
+        if self.graph:
+            g, self.graph = self.graph, None
+            Hip.check(h.hipGraphDestroy(g), "hipGraphDestroy")
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
+        return False
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 class DeviceBuffer:
     """Owned device allocation."""
 
+    _live: set = set()  # serials of the buffers allocated and not yet freed
+    _serial = 0
+
     def __init__(self, nbytes: int):
         self.nbytes = int(nbytes)
+        self.ptr = None
         p = C.c_void_p()
         Hip.check(Hip.lib().hipMalloc(C.byref(p), max(self.nbytes, 1)), f"hipMalloc({self.nbytes})")
         self.ptr = p.value
+        DeviceBuffer._serial += 1
+        self.serial = DeviceBuffer._serial
+        DeviceBuffer._live.add(self.serial)
 
     @classmethod
     def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
@@ -213,24 +279,35 @@ class DeviceBuffer:
 
     def upload(self, a: np.ndarray, offset: int = 0):
         a = np.ascontiguousarray(a)
-        assert offset + a.nbytes <= self.nbytes
+        assert self.ptr and offset + a.nbytes <= self.nbytes
         Hip.check(Hip.lib().hipMemcpy(self.ptr + offset, a.ctypes.data, a.nbytes, 1), "hipMemcpy H2D")
 
     def download(self, shape, dtype, offset: int = 0) -> np.ndarray:
         out = np.empty(shape, dtype)
-        assert offset + out.nbytes <= self.nbytes
+        assert self.ptr and offset + out.nbytes <= self.nbytes
         Hip.check(Hip.lib().hipMemcpy(out.ctypes.data, self.ptr + offset, out.nbytes, 2), "hipMemcpy D2H")
         return out
 
     def fill_bytes(self, value: int):
         Hip.check(Hip.lib().hipMemset(self.ptr, value, self.nbytes), "hipMemset")
 
+    def captured_by_live_graph(self) -> bool:
+        return any(self.serial in g.captured for g in _live_graphs.values())
+
     def free(self):
+        """Free the allocation. Raises while a live Graph may reference it (destroy the
+        graph first)."""
         if self.ptr:
-            Hip.lib().hipFree(self.ptr)
-            self.ptr = None
+            if self.captured_by_live_graph():
+                raise RuntimeError(f"DeviceBuffer({self.nbytes} B) freed while a live Graph captured with it "
+                                   f"exists: destroy the graph first")
+            p, self.ptr = self.ptr, None
+            DeviceBuffer._live.discard(self.serial)
+            Hip.check(Hip.lib().hipFree(p), "hipFree")
 
     def __del__(self):
+        # a buffer collected while a live graph may still use it stays allocated (a leak,
+        # never a dangling pointer)
         try:
             self.free()
         except Exception:
@@ -253,6 +330,17 @@ class Event:
         ms = C.c_float()
         Hip.check(Hip.lib().hipEventElapsedTime(C.byref(ms), self.e, end.e), "hipEventElapsedTime")
         return ms.value
+
+    def destroy(self):
+        if self.e:
+            e, self.e = self.e, None
+            Hip.check(Hip.lib().hipEventDestroy(e), "hipEventDestroy")
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 # ------------------------------------------------- friday_attn launcher mirror
@@ -322,6 +410,17 @@ def decodeWorkspaceInit(workspace, workspace_bytes=None, stream=None):
     if workspace_bytes is None:
         workspace_bytes = workspace.nbytes
     _check(load().friday_attn_decode_workspace_init(_ptr(workspace), workspace_bytes, stream))
+
+
+def decodeWorkspaceStatus(workspace, workspace_bytes=None, stream=None) -> int:
+    """FA_OK, or FA_ERR_TIMEOUT once a fused merge on this workspace gave up waiting
+    (synchronises `stream`)."""
+    if workspace_bytes is None:
+        workspace_bytes = workspace.nbytes
+    rc = load().friday_attn_decode_workspace_status(_ptr(workspace), workspace_bytes, stream)
+    if rc not in (FA_OK, FA_ERR_TIMEOUT):
+        _check(rc)
+    return rc
 
 
 def launchDecodeAttentionFused(q, k_cache, v_cache, out, seq_len, d_pos, max_seq_len, num_heads, num_kv_heads,

@@ -39,6 +39,7 @@ extern "C" {
 #define FA_ERR_UNSUPPORTED (-2) /* valid but not implemented for these shapes */
 #define FA_ERR_LAUNCH (-3)      /* a HIP launch or copy failed */
 #define FA_ERR_WORKSPACE (-4)   /* workspace too small or missing */
+#define FA_ERR_TIMEOUT (-5)     /* a fused merge gave up waiting (friday_attn_decode_workspace_status) */
 
 #define FA_PAGE_TOKENS 16 /* paged_kv_cache.h:16 KV_BLOCK_SIZE */
 
@@ -113,6 +114,15 @@ int friday_attn_decode_attention_split(const uint16_t* q, const void* k_cache, c
  * split partials after them; a contiguous call counts as batch 1): calls with another
  * batch size or head count may share it only after it is initialised again. */
 int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+/* No counterpart in the reference (its merge is a second kernel and cannot wait). The
+ * fused merge waits, bounded (1 s), for every split of its group to arrive; a merger that
+ * gives up sets a sticky error word in the workspace and merges nothing, so that call's
+ * output and rotated q are not written, and the workspace's counters are no longer in step.
+ * This query (a 4-byte copy and a synchronisation of `stream`: not for use under capture)
+ * returns FA_ERR_TIMEOUT once that has happened on `workspace`, FA_OK otherwise;
+ * friday_attn_decode_workspace_init clears it. Covers every call that takes a workspace
+ * (fused, step, int8 step, quant step, paged). */
+int friday_attn_decode_workspace_status(const void* workspace, size_t workspace_bytes, void* stream);
 /* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
  * few workgroups of each kv head (the ones dispatched last), each over a slice of the
  * columns, once an arrival counter in the workspace shows every split stored, instead
@@ -142,8 +152,9 @@ int friday_attn_decode_step(uint16_t* q, const uint16_t* k, const uint16_t* v, u
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
  * friday_attn_decode_step with the workspace replaced by a scratch the library holds in
  * device memory, 4 MiB per GPU: 1 MiB of counter slots (up to 4096 query heads) and 3 MiB
- * of split partials. Allocates nothing; the first call on a device looks the scratch up and
- * zeroes it with a fill kernel on `stream`. Results are bit-identical to
+ * of split partials. Allocates nothing and launches nothing but the step: the scratch is zero
+ * when the library's code object loads, and the first call on a device only looks up its
+ * address, so that call may be made under stream capture. Results are bit-identical to
  * friday_attn_decode_step. All calls on one GPU share its scratch, whatever their head
  * counts: calls that overlap (other streams, concurrent graph replays) race and must be
  * serialised by the caller. FA_ERR_WORKSPACE when the call would need more than that. */

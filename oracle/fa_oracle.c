@@ -400,6 +400,115 @@ void or_prefill_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const
                    Hkv * hd, 1);
 }
 
+/* ---- the same prefill rows, blocked for speed (test infrastructure) ----
+ *
+ * or_prefill_rows_f32 computes rows of or_prefill_attention / _q8 / _bf16 with the very
+ * same fp32 operations per output value: the cache values are widened once
+ * (or_prefill_widen: the exact fp16 / bf16 value, or the int8 code times its fp16 scale in
+ * one fp32 product, as get_q8 forms it), K is stored transposed per kv head so that the dot
+ * products of many positions and query heads are formed side by side, and every dot
+ * product still accumulates q[d] * k[d] in increasing d from 0.0f, every softmax sum runs
+ * over increasing p, and every output column sums w * v over increasing p. Only the
+ * loop nesting differs, which changes no rounding (contraction is off). Pinned bit for bit
+ * against the row-by-row functions in tests/test_oracle.py. */
+
+/* kt[(h * hd + d) * S + p] and vf[(p * Hkv + h) * hd + d] from a cache of any kind */
+void or_prefill_widen(const void* kc, const uint16_t* ks, const void* vc, const uint16_t* vs, int kind, int S,
+                      int Hkv, int hd, float* kt, float* vf) {
+    kv_get_fn get = kind == 1 ? get_q8 : (kind == 2 ? get_bf16 : get_f16);
+    const int kv = Hkv * hd;
+    for (int p = 0; p < S; ++p)
+        for (int h = 0; h < Hkv; ++h)
+            for (int d = 0; d < hd; ++d) {
+                const size_t i = (size_t)p * kv + (size_t)h * hd + d;
+                kt[((size_t)h * hd + d) * S + p] = get(kc, ks, i);
+                vf[i] = get(vc, vs, i);
+            }
+}
+
+#define OR_PB 256 /* positions per score block */
+
+/* rows t0 .. t0 + T - 1 of a chunk whose row t attends positions [0, p0 + t]; q holds the T
+ * rows ([T][Hq * hd], fp16 or bf16 bits), kt / vf come from or_prefill_widen over Smax >=
+ * p0 + t0 + T positions; bf16 != 0: bf16 q and the bf16 output rule */
+void or_prefill_rows_f32(const uint16_t* q, const float* kt, const float* vf, int Smax, float* out, int T, int p0,
+                         int Hq, int Hkv, int hd, int bf16) {
+    const int G = Hq / Hkv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int Slast = p0 + T; /* positions the last row attends */
+    float* qf = (float*)malloc(sizeof(float) * (size_t)T * G * hd);
+    float* s = (float*)malloc(sizeof(float) * (size_t)T * G * (Slast > 0 ? Slast : 1));
+    float* acc = (float*)malloc(sizeof(float) * (size_t)T * G * hd);
+    for (int h = 0; h < Hkv; ++h) {
+        /* the T x G queries of this kv head, widened */
+        for (int t = 0; t < T; ++t)
+            for (int g = 0; g < G; ++g)
+                for (int d = 0; d < hd; ++d) {
+                    const uint16_t x = q[(size_t)t * Hq * hd + (size_t)(h * G + g) * hd + d];
+                    qf[((size_t)t * G + g) * hd + d] = bf16 ? or_bf16_to_float(x) : or_half_to_float(x);
+                }
+        /* scores: s[j][p] = sum_d qf[j][d] * k[p][d] in increasing d, for p < the row's length */
+        for (int pb = 0; pb < Slast; pb += OR_PB) {
+            const int pe = pb + OR_PB < Slast ? pb + OR_PB : Slast;
+            for (int j = 0; j < T * G; ++j) {
+                float* sj = s + (size_t)j * Slast;
+                for (int p = pb; p < pe; ++p) sj[p] = 0.0f;
+            }
+            for (int d = 0; d < hd; ++d) {
+                const float* kr = kt + ((size_t)h * hd + d) * Smax;
+                for (int j = 0; j < T * G; ++j) {
+                    const int Sj = p0 + j / G + 1;
+                    if (pb >= Sj) continue;
+                    const int e = pe < Sj ? pe : Sj;
+                    const float qd = qf[(size_t)j * hd + d];
+                    float* sj = s + (size_t)j * Slast;
+                    for (int p = pb; p < e; ++p) sj[p] += qd * kr[p];
+                }
+            }
+        }
+        /* softmax per query in increasing p, then acc[d] += w * v[p][d] in increasing p */
+        for (int j = 0; j < T * G; ++j) {
+            const int Sj = p0 + j / G + 1;
+            float* sj = s + (size_t)j * Slast;
+            float mx = -1e30f;
+            for (int p = 0; p < Sj; ++p) {
+                float dot = sj[p] * scale;
+                if (isnan(dot)) dot = -1e30f;
+                sj[p] = dot;
+                if (dot > mx) mx = dot;
+            }
+            float sum = 0.0f;
+            for (int p = 0; p < Sj; ++p) {
+                const float df = sj[p] - mx;
+                sj[p] = df < -50.0f ? 0.0f : expf(df);
+                sum += sj[p];
+            }
+            const float inv = sum > 1e-12f ? 1.0f / sum : 0.0f;
+            for (int p = 0; p < Sj; ++p) sj[p] *= inv;
+            float* aj = acc + (size_t)j * hd;
+            for (int d = 0; d < hd; ++d) aj[d] = 0.0f;
+        }
+        for (int p = 0; p < Slast; ++p) {
+            const float* vr = vf + ((size_t)p * Hkv + h) * hd;
+            for (int j = 0; j < T * G; ++j) {
+                if (p >= p0 + j / G + 1) continue;
+                const float w = s[(size_t)j * Slast + p];
+                float* aj = acc + (size_t)j * hd;
+                for (int d = 0; d < hd; ++d) aj[d] += w * vr[d];
+            }
+        }
+        for (int j = 0; j < T * G; ++j) {
+            const int t = j / G, g = j % G;
+            float* o = out + (size_t)t * Hq * hd + (size_t)(h * G + g) * hd;
+            const float* aj = acc + (size_t)j * hd;
+            for (int d = 0; d < hd; ++d) o[d] = bf16 ? or_round_to_bf16(aj[d]) : or_round_to_half(aj[d]);
+        }
+    }
+    free(qf);
+    free(s);
+    free(acc);
+}
+
 /* ---- paged addressing (paged_attention.cu:29-41: phys = table[pos/16], row pos%16) ---- */
 
 void or_paged_gather(const uint16_t* pool, const int32_t* block_table, int S, int page, int kv_dim, uint16_t* dst) {

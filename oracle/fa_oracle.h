@@ -78,6 +78,13 @@ void or_prefill_attention(const uint16_t* q, const uint16_t* k_cache, const uint
                           int p0, int Hq, int Hkv, int head_dim);
 void or_prefill_attention_q8(const uint16_t* q, const int8_t* k_cache, const uint16_t* k_scale, const int8_t* v_cache,
                              const uint16_t* v_scale, float* out, int T, int p0, int Hq, int Hkv, int head_dim);
+/* Blocked evaluation of the prefill rows above with the same fp32 operations per value
+ * (test infrastructure for checking whole chunks): widen a cache once (kind 0 fp16, 1 int8
+ * with scales, 2 bf16) into kt [Hkv][hd][S] and vf [S][Hkv*hd], then compute rows. */
+void or_prefill_widen(const void* kc, const uint16_t* ks, const void* vc, const uint16_t* vs, int kind, int S,
+                      int Hkv, int hd, float* kt, float* vf);
+void or_prefill_rows_f32(const uint16_t* q, const float* kt, const float* vf, int Smax, float* out, int T, int p0,
+                         int Hq, int Hkv, int hd, int bf16);
 /* or_prefill_attention with bf16 q / caches and the bf16 output rule (no reference counterpart) */
 void or_prefill_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int T,
                                int p0, int Hq, int Hkv, int hd);

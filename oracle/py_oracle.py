@@ -67,6 +67,8 @@ class Oracle:
         L.or_prefill_attention_bf16.argtypes = [_u16p, _u16p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_prefill_attention_q8.argtypes = [_u16p, _i8p, _u16p, _i8p, _u16p, _f32p, _i, _i, _i, _i, _i]
         L.or_paged_gather.argtypes = [_u16p, _i32p, _i, _i, _i, _u16p]
+        L.or_prefill_widen.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _i, _i, _i, _i, _f32p, _f32p]
+        L.or_prefill_rows_f32.argtypes = [_u16p, _f32p, _f32p, _i, _f32p, _i, _i, _i, _i, _i, _i]
         L.or_q8_row_bytes.restype = C.c_size_t
         L.or_q8_row_bytes.argtypes = [_i, _i]
         L.or_quantize_q8_rows.argtypes = [_u16p, _i, _i, _i8p, _f32p]
@@ -162,6 +164,39 @@ class Oracle:
         out = np.empty((T, Hq * d), np.float32)
         self.lib.or_prefill_attention_q8(_f16bits(q).ravel(), k8.ravel(), _f16bits(ks).ravel(), v8.ravel(),
                                          _f16bits(vs).ravel(), out.ravel(), T, p0, Hq, Hkv, d)
+        return out
+
+    def prefill_all(self, q, kc, vc, T, p0, Hq, Hkv, d, ks=None, vs=None, bf16=False, block=16,
+                    workers=16) -> np.ndarray:
+        """Every row of prefill / prefill_q8 (ks, vs given: int8 codes kc / vc) / prefill_bf16, bit
+        for bit, by the blocked evaluator (or_prefill_rows_f32) on `workers` threads over row
+        blocks (the C calls release the GIL)."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        S = p0 + T
+        kind = 1 if ks is not None else (2 if bf16 else 0)
+        kt = np.empty(S * Hkv * d, np.float32)
+        vf = np.empty(S * Hkv * d, np.float32)
+        if kind == 1:
+            kk, vv = np.ascontiguousarray(kc[:S], np.int8), np.ascontiguousarray(vc[:S], np.int8)
+            kss, vss = _f16bits(ks[:S]).ravel(), _f16bits(vs[:S]).ravel()
+            self.lib.or_prefill_widen(kk.ctypes.data, kss.ctypes.data, vv.ctypes.data, vss.ctypes.data, 1, S, Hkv, d,
+                                      kt, vf)
+        else:
+            kk = np.ascontiguousarray(kc[:S], np.uint16).ravel()
+            vv = np.ascontiguousarray(vc[:S], np.uint16).ravel()
+            self.lib.or_prefill_widen(kk.ctypes.data, None, vv.ctypes.data, None, kind, S, Hkv, d, kt, vf)
+        qq = np.ascontiguousarray(q, np.uint16).reshape(T, Hq * d)
+        out = np.empty((T, Hq * d), np.float32)
+
+        def rows(t0):
+            n = min(block, T - t0)
+            self.lib.or_prefill_rows_f32(qq[t0:t0 + n].ravel(), kt, vf, S, out[t0:t0 + n].ravel(), n, p0 + t0, Hq,
+                                         Hkv, d, int(bf16))
+
+        starts = list(range(0, T, block))
+        with ThreadPoolExecutor(max_workers=max(1, min(workers, len(starts)))) as ex:
+            list(ex.map(rows, starts))
         return out
 
     def paged_gather(self, pool, block_table, S, page, kv_dim) -> np.ndarray:

@@ -83,3 +83,4 @@ def assert_gemm_close(got, ref, what=""):
     max_rel = np.max(np.abs(d)) / np.sqrt(den / ref.size + 1e-30)
     assert rel < GEMM_REL_L2 and max_rel < GEMM_MAX_REL, f"{what}: rel_l2 {rel:.2e} max_rel {max_rel:.2e}"
     return rel, max_rel
+

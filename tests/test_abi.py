@@ -203,3 +203,31 @@ def test_gemv_q8_validation(fa):
     assert L.friday_gemv_q8(fa.Q8_0, FAKE, FAKE, FAKE, 96, 0, FAKE, None, None, None, None, None) == fa.FA_ERR_INVALID
     assert L.friday_gemv_q8(fa.Q8_0, FAKE + 2, FAKE, FAKE, 96, 8, FAKE, None, None, None, None, None) == \
         fa.FA_ERR_INVALID
+
+
+def test_decode_alignment_and_status_checks(fa):
+    """The decode paths move q, the caches and the new rows as 16-byte chunks and the
+    output as 8-byte ones: misaligned pointers are refused before any launch."""
+    L = fa.load()
+    ws = 1 << 30
+    assert L.friday_attn_decode_step(FAKE + 2, FAKE, FAKE, FAKE, FAKE, FAKE, None, 5, 10, 40, 8, 128, FAKE, 1, FAKE,
+                                     ws, None) == fa.FA_ERR_INVALID
+    assert "aligned" in err(fa)
+    assert L.friday_attn_decode_step(FAKE, FAKE + 8, FAKE, FAKE, FAKE, FAKE, None, 5, 10, 40, 8, 128, FAKE, 1, FAKE,
+                                     ws, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_decode_step(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE + 4, None, 5, 10, 40, 8, 128, FAKE, 1, FAKE,
+                                     ws, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_decode_step_q8(FAKE, FAKE, FAKE, FAKE + 1, FAKE, FAKE, FAKE, FAKE, None, 5, 10, 40, 8, 128,
+                                        FAKE, 1, FAKE, ws, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_decode_step_noalloc(FAKE, FAKE, FAKE, FAKE, FAKE + 2, FAKE, None, 5, 10, 40, 8, 128, FAKE, 1,
+                                             None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_decode_attention_fused(FAKE + 2, FAKE, FAKE, FAKE, 5, None, 10, 40, 8, 128, FAKE, ws, None,
+                                                None, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_decode_attention(FAKE, FAKE, FAKE + 8, FAKE, 5, 40, 8, 128, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_paged_decode_step(FAKE, FAKE + 2, FAKE, FAKE, FAKE, FAKE, FAKE, 256, FAKE, 4, 4096, 40, 8,
+                                           128, FAKE, 1, FAKE, ws, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_paged_decode_attention(FAKE, FAKE + 4, FAKE, FAKE, FAKE, 256, FAKE, 4, 4096, 40, 8, 128,
+                                                FAKE, ws, None) == fa.FA_ERR_INVALID
+    # the status query needs a workspace that holds counter slot 0
+    assert L.friday_attn_decode_workspace_status(None, 4096, None) == fa.FA_ERR_INVALID
+    assert L.friday_attn_decode_workspace_status(FAKE, 16, None) == fa.FA_ERR_INVALID

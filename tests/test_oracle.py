@@ -324,3 +324,49 @@ def test_paged_gather(oracle):
         n = min(page, S - j * page)
         pool[perm[j], :n] = rows[j * page:j * page + n]
     assert np.array_equal(oracle.paged_gather(pool, perm, S, page, kv_dim), rows)
+
+
+@pytest.mark.parametrize("Hq,Hkv,d,T,p0", [(8, 2, 64, 37, 21), (40, 8, 128, 40, 300), (16, 1, 128, 3, 0),
+                                            (48, 3, 64, 20, 5)])
+def test_blocked_prefill_equals_row_by_row(oracle, Hq, Hkv, d, T, p0):
+    """The blocked evaluator the GPU tests use for whole config-4 chunks (prefill_all:
+    or_prefill_widen + or_prefill_rows_f32 over threaded row blocks) gives the row-by-row
+    oracle prefill bit for bit: fp16, int8 and bf16 caches, with a NaN key row, an all-NaN
+    query row, an outlier key and a score block boundary inside the rows."""
+    from fa_helpers import f16
+
+    rng = np.random.default_rng(11 + T)
+    S = p0 + T
+    q = f16(rng, (T, Hq * d))
+    k, v = f16(rng, (S, Hkv * d)), f16(rng, (S, Hkv * d))
+    k[S // 2] = 0x7E00  # NaN key row
+    k[S // 3, :d] = np.float16(40.0).view(np.uint16)  # outlier key of kv head 0
+    q[T // 2] = 0x7E00  # every score of this row NaN
+    for blk, workers in ((16, 16), (5, 3), (1, 2)):
+        want = oracle.prefill(q, k, v, T, p0, Hq, Hkv, d)
+        got = oracle.prefill_all(q, k, v, T, p0, Hq, Hkv, d, block=blk, workers=workers)
+        assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), f"fp16 block={blk}"
+        wb = oracle.prefill_bf16(q, k, v, T, p0, Hq, Hkv, d)
+        gb = oracle.prefill_all(q, k, v, T, p0, Hq, Hkv, d, bf16=True, block=blk, workers=workers)
+        assert np.array_equal(wb.view(np.uint32), gb.view(np.uint32)), f"bf16 block={blk}"
+    k8 = rng.integers(-127, 128, (S, Hkv * d), dtype=np.int8)
+    v8 = rng.integers(-127, 128, (S, Hkv * d), dtype=np.int8)
+    ks = rng.uniform(0.001, 0.02, (S, Hkv * d // 32)).astype(np.float16).view(np.uint16)
+    vs = rng.uniform(0.001, 0.02, (S, Hkv * d // 32)).astype(np.float16).view(np.uint16)
+    wq = oracle.prefill_q8(q, k8, ks, v8, vs, T, p0, Hq, Hkv, d)
+    gq = oracle.prefill_all(q, k8, v8, T, p0, Hq, Hkv, d, ks=ks, vs=vs, block=7, workers=4)
+    assert np.array_equal(wq.view(np.uint32), gq.view(np.uint32))
+
+
+def test_blocked_prefill_long_prefix(oracle):
+    """Several 256-position score blocks and a long prefix (the config-4 regime), against the
+    row-by-row oracle on a few rows."""
+    from fa_helpers import f16
+
+    rng = np.random.default_rng(3)
+    Hq, Hkv, d, T, p0 = 40, 8, 128, 24, 1500
+    q = f16(rng, (T, Hq * d))
+    k, v = f16(rng, (p0 + T, Hkv * d)), f16(rng, (p0 + T, Hkv * d))
+    got = oracle.prefill_all(q, k, v, T, p0, Hq, Hkv, d)
+    want = oracle.prefill(q, k, v, T, p0, Hq, Hkv, d)
+    assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
