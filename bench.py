@@ -22,7 +22,9 @@ on this host.
 --config all additionally prints one JSON line per other benchmark config
 (1: Qwen2.5-0.5B shapes; 2: 32 layers at 1k/4k/8k, cold and warm; 3 at 16k;
 4: chunked prefill on MFMA with MFMA utilisation; 5: 16 paged sequences), the int8-KV step,
-the RoPE + KV append rows (T = 1 and 512), and the matmuls either side of attention;
+the RoPE + KV append rows (T = 1 and 512, fp16 and int8), the prefill launch against T
+single-token decode launches (the reference's own comparison), and the matmuls either
+side of attention;
 --config short prints configs 1 and 2 only.
 """
 from __future__ import annotations
@@ -396,6 +398,74 @@ def prefill_config(cx, p0, steps, warmup, q8=False, bf16=False):
             "mfma_utilisation": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "tokens_per_s": round(T / (ms * 1e-3), 0)}
 
 
+def prefill_vs_decode_config(cx, p0, steps, warmup):
+    """The reference's own comparison (tests/kernels/test_prefill_attention.cu:89-107): one
+    512-token chunk after p0 cached tokens, once as T single-token split decodes (row t
+    attends p0 + t + 1 positions, its position read from device memory, the merge in a second
+    kernel as launchDecodeAttentionSplit does) and once as one prefill launch; 40q/8kv d128,
+    fp16 KV, one cache (warm, as in the reference bench). Both are graph replays."""
+    import numpy as np
+
+    fa = cx.fa
+    T, Hq, Hkv, d = 512, 40, 8, 128
+    S = p0 + T
+    kv_dim = Hkv * d
+    k, v = fa.DeviceBuffer(S * kv_dim * 2), fa.DeviceBuffer(S * kv_dim * 2)
+    cx.fill(k, S * kv_dim, 5)
+    cx.fill(v, S * kv_dim, 6)
+    q, out = fa.DeviceBuffer(T * Hq * d * 2), fa.DeviceBuffer(T * Hq * d * 2)
+    cx.fill(q, T * Hq * d, 7)
+    pos0 = fa.DeviceBuffer.from_array(np.array([p0], np.int32))
+    rows = fa.DeviceBuffer.from_array(np.arange(p0, p0 + T, dtype=np.int32))  # row t: *d_pos = p0 + t
+    ws = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, S))
+    qd = Hq * d * 2
+
+    def per_token():
+        for t in range(T):
+            fa.launchDecodeAttentionSplit(q.ptr + t * qd, k, v, out.ptr + t * qd, 0, rows.ptr + 4 * t, S, Hq, Hkv, d,
+                                          ws, cx.stream.s)
+
+    ms_dec = cx.timed(per_token, steps, warmup)
+    ms_pf = cx.timed(lambda: fa.launchPrefillAttention(q, k, v, out, T, pos0, Hq, Hkv, d, cx.stream.s), steps, warmup)
+    for b in (k, v, q, out, pos0, rows, ws):
+        b.free()
+    return {"config": "4: prefill launch vs T single-token decode launches (test_prefill_attention.cu --bench)",
+            "T": T, "p0": p0, "heads": f"{Hq}q/{Hkv}kv d{d}", "per_token_decode_us": round(ms_dec * 1e3, 1),
+            "prefill_us": round(ms_pf * 1e3, 2), "prefill_speedup": round(ms_dec / ms_pf, 1)}
+
+
+def append_q8_config(cx, T, steps, warmup):
+    """int8 KV append (friday_attn_store_kv_q8, storeKvQ8Kernel semantics: already-rotated k and
+    v quantised per 32 values) at the headline shapes (8 kv heads, d128): T = 1 or 512, one
+    launch per layer over 64 layers. Algorithmic bytes per token: k and v read as fp16
+    (2 kv_dim 2), int8 rows and fp16 scales written (2 kv_dim + 2 (kv_dim / 32) 2)."""
+    import numpy as np
+
+    fa = cx.fa
+    Hkv, d, L, max_ctx = 8, 128, 64, 8192
+    kv_dim = Hkv * d
+    k, v = fa.DeviceBuffer(L * T * kv_dim * 2), fa.DeviceBuffer(L * T * kv_dim * 2)
+    cx.fill(k, L * T * kv_dim, 40)
+    cx.fill(v, L * T * kv_dim, 41)
+    lb, sb = max_ctx * kv_dim, max_ctx * (kv_dim // 32) * 2
+    k8, v8, ks, vs = fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * sb), fa.DeviceBuffer(L * sb)
+    pos = fa.DeviceBuffer.from_array(np.array([max_ctx - T - 1], np.int32))
+
+    def run():
+        for l in range(L):
+            fa.storeKvQ8(k.ptr + l * T * kv_dim * 2, v.ptr + l * T * kv_dim * 2, k8.ptr + l * lb, ks.ptr + l * sb,
+                         v8.ptr + l * lb, vs.ptr + l * sb, pos, 0, T, kv_dim, max_ctx, cx.stream.s)
+
+    ms = cx.timed(run, steps, warmup) / L
+    for bb in (k, v, k8, v8, ks, vs, pos):
+        bb.free()
+    per_token = 2 * kv_dim * 2 + 2 * kv_dim + 2 * (kv_dim // 32) * 2
+    gbs = T * per_token / (ms * 1e-3) / 1e9
+    return {"config": "int8 KV append (storeKvQ8Kernel)", "T": T, "heads": f"{Hkv}kv d{d}",
+            "us_per_layer": round(ms * 1e3, 3), "bytes_per_layer": T * per_token, "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 # The reference's GEMM bench shapes (test_prefill_gemm.cu:40-42): kind code, K, N, what
 GEMM_CASES = [(3, 4096, 14336, "8B ffn_gate Q4_K"), (5, 14336, 4096, "8B ffn_down Q6_K"),
               (1, 5120, 27648, "32B ffn_gate Q2_K"), (2, 27648, 5120, "32B ffn_down Q3_K")]
@@ -669,6 +739,10 @@ def main():
         emit(paged_config(cx, args.steps, args.warmup))
         for T in (1, 512):
             emit(append_config(cx, T, args.steps, args.warmup))
+        for T in (1, 512):
+            emit(append_q8_config(cx, T, args.steps, args.warmup))
+        for p0 in (0, 7680):
+            emit(prefill_vs_decode_config(cx, p0, args.steps, args.warmup))
         emit(q8_config(cx, 32768, 64, args.steps, args.warmup))
         for case in GEMM_CASES:
             emit(gemm_config(cx, *case, args.steps, args.warmup))
@@ -681,6 +755,8 @@ def main():
     if args.config == "append":
         for T in (1, 512):
             print(json.dumps(append_config(cx, T, args.steps, args.warmup)), flush=True)
+        for T in (1, 512):
+            print(json.dumps(append_q8_config(cx, T, args.steps, args.warmup)), flush=True)
     if args.config == "paged":
         print(json.dumps(paged_config(cx, args.steps, args.warmup)), flush=True)
     if args.config == "prefill":
@@ -690,6 +766,8 @@ def main():
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup, q8=True)), flush=True)
         for p0 in (0, 1024, 2048, 4096, 7680):
             print(json.dumps(prefill_config(cx, p0, args.steps, args.warmup, bf16=True)), flush=True)
+        for p0 in (0, 7680):
+            print(json.dumps(prefill_vs_decode_config(cx, p0, args.steps, args.warmup)), flush=True)
     if args.config == "layer":
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True)), flush=True)

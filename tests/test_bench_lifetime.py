@@ -209,6 +209,8 @@ def test_bench_sequence_frees_nothing_a_live_graph_uses(fake_fa):
     bench.paged_config(cx, 2, 1, L=2)
     for T in (1, 512):
         bench.append_config(cx, T, 2, 1)
+        bench.append_q8_config(cx, T, 2, 1)
+    bench.prefill_vs_decode_config(cx, 1024, 2, 1)
     bench.q8_config(cx, 2048, 2, 2, 1)
     bench.gemv_config(cx, *bench.GEMV_CASES[0], 2, 1)
     bench.layer_block_config(cx, 2048, 2, 2, 1)
