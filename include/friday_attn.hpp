@@ -57,6 +57,15 @@ inline bool decodeAttentionFitsSharedMemory(int max_seq_len) {
 inline size_t splitAttentionWorkspaceBytes(int num_heads, int max_seq_len) {
     return friday_attn_split_workspace_bytes(num_heads, max_seq_len);
 }
+// No counterpart in the reference: health of a fused-merge workspace (throws on a launch
+// error; returns false once a fused merge gave up waiting, true otherwise). Synchronises
+// `stream`; not for use under capture.
+inline bool decodeWorkspaceHealthy(const void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const int rc = friday_attn_decode_workspace_status(workspace, workspace_bytes, stream);
+    if (rc == FA_ERR_TIMEOUT) return false;
+    detail::check(rc);
+    return true;
+}
 inline void launchDecodeAttentionSplit(const void* q, const void* k_cache, const void* v_cache, void* out,
                                        int seq_len, const int* d_pos, int max_seq_len, int num_heads,
                                        int num_kv_heads, int head_dim, void* workspace, hipStream_t stream,
