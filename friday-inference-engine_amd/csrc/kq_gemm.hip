@@ -804,12 +804,12 @@ int launch_kq_shape(int kind, const KqGemmParams& p, hipStream_t stream) {
 
 }  // namespace
 
-// Tile shape: 256 x 128 (eight waves, one workgroup per CU) when that alone fills the 256
-// CUs, else 128 x 128 (four waves, two per CU) when it gives at least 1.5 workgroups per
+// Tile shape: 256 x 128 (eight waves, one workgroup per CU) when that alone fills the
+// device's CUs (256 on an MI355X), else 128 x 128 (four waves, two per CU) when it gives at least 1.5 workgroups per
 // CU, else 64 x 64 (four waves, one tile each) so that small-N / large-K shapes still
 // spread over the chip. FRIDAY_GEMM_TILE = 1 / 2 / 3 forces one of them.
 // K split for shapes that fill neither tile: 128 x 128 tiles with the split count (2 to 8,
-// at least 16 stages of 64 K values each) that best fills 512 workgroup slots (two per
+// at least 16 stages of 64 K values each) that best fills the workgroup slots (two per
 // CU), the smaller count on ties. FRIDAY_GEMM_KSPLIT = 1 turns it off, n > 1 forces n.
 KqPlan kq_gemm_plan(int T, int K, int N) {
     static const int forced = [] {
@@ -823,14 +823,15 @@ KqPlan kq_gemm_plan(int T, int K, int N) {
     auto wgs = [&](int bn, int bt) { return (long)((N + bn - 1) / bn) * ((T + bt - 1) / bt); };
     const int nst = K / kGBK;
     const long tiles = wgs(128, 128);
+    const long cus = device_cus(), slots = 2 * cus;  // two 128 x 128 workgroups per CU
     int best = 1;
     if (forced > 1) {
         best = forced;
-    } else if (forced == 0 && wgs(256, 128) < 256 && tiles < 384) {
+    } else if (forced == 0 && wgs(256, 128) < cus && 2 * tiles < 3 * cus) {
         double fill_best = 0.0;
         for (int sk = 2; sk <= 8 && nst / sk >= 16; ++sk) {
             const long n = tiles * sk;
-            const double fill = (double)n / (512.0 * ((n + 511) / 512));
+            const double fill = (double)n / ((double)slots * ((n + slots - 1) / slots));
             if (fill > fill_best + 1e-9) fill_best = fill, best = sk;
         }
     }
@@ -854,7 +855,8 @@ int launch_kq_gemm(int kind, const KqGemmParams& p, hipStream_t stream) {
     if (p.ksplit > 1) return launch_kq_shape<2, 2, 2, 2>(kind, p, stream);
     auto wgs = [&](int bn, int bt) { return (long)((p.N + bn - 1) / bn) * ((p.T + bt - 1) / bt); };
     int shape = forced;
-    if (shape < 1 || shape > 4) shape = wgs(256, 128) >= 256 ? 1 : (wgs(128, 128) >= 384 ? 2 : 3);
+    const long cus = device_cus();
+    if (shape < 1 || shape > 4) shape = wgs(256, 128) >= cus ? 1 : (2 * wgs(128, 128) >= 3 * cus ? 2 : 3);
     if (shape == 1) return launch_kq_shape<4, 2, 2, 2>(kind, p, stream);
     if (shape == 2) return launch_kq_shape<2, 2, 2, 2>(kind, p, stream);
     if (shape == 4) return launch_kq_shape<2, 4, 2, 1>(kind, p, stream);
