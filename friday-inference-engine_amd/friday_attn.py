@@ -192,6 +192,18 @@ class Stream:
 # those buffers while the graph lives would leave the graph pointing at memory that the
 # next allocation reuses, so DeviceBuffer.free() refuses it.
 _live_graphs: dict = {}
+_deferred_frees: list = []  # (ptr, serial) of collected buffers that a live graph captured
+
+
+def _release_deferred():
+    keep = []
+    for ptr, serial in _deferred_frees:
+        if any(serial in g.captured for g in _live_graphs.values()):
+            keep.append((ptr, serial))
+        else:
+            DeviceBuffer._live.discard(serial)
+            Hip.lib().hipFree(ptr)
+    _deferred_frees[:] = keep
 
 
 class Graph:
@@ -239,6 +251,7 @@ class Graph:
         if self.graph:
             g, self.graph = self.graph, None
             Hip.check(h.hipGraphDestroy(g), "hipGraphDestroy")
+        _release_deferred()
 
     def __enter__(self):
         return self
@@ -306,10 +319,14 @@ class DeviceBuffer:
             Hip.check(Hip.lib().hipFree(p), "hipFree")
 
     def __del__(self):
-        # a buffer collected while a live graph may still use it stays allocated (a leak,
-        # never a dangling pointer)
+        # a buffer collected while a live graph may still use it is freed when the last such
+        # graph is destroyed (never earlier: no dangling pointer)
         try:
-            self.free()
+            if self.ptr and self.captured_by_live_graph():
+                _deferred_frees.append((self.ptr, self.serial))
+                self.ptr = None
+            else:
+                self.free()
         except Exception:
             pass
 

@@ -179,6 +179,7 @@ def fake_fa(monkeypatch):
     monkeypatch.setattr(fa.Hip, "_h", hip)
     monkeypatch.setattr(fa.DeviceBuffer, "_live", set())
     monkeypatch.setattr(fa, "_live_graphs", {})
+    monkeypatch.setattr(fa, "_deferred_frees", [])
     return fa, hip
 
 
@@ -248,3 +249,20 @@ def test_graph_context_manager_releases(fake_fa):
     buf.free()
     st.destroy()
     assert hip.violations == [] and hip.allocs == {} and hip.streams == set()
+
+
+def test_collected_buffer_freed_after_its_graph(fake_fa):
+    """A buffer collected while a live graph captured it is not freed then, but as soon as
+    that graph is destroyed."""
+    import gc
+
+    fa, hip = fake_fa
+    st = fa.Stream()
+    buf = fa.DeviceBuffer(4096)
+    ptr = buf.ptr
+    g = fa.Graph(st, lambda: fa.decodeWorkspaceInit(buf, stream=st.s))
+    del buf
+    gc.collect()
+    assert ptr in hip.allocs and hip.violations == []
+    g.destroy()
+    assert ptr not in hip.allocs and hip.violations == []
