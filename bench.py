@@ -684,6 +684,71 @@ def paged_config(cx, steps, warmup, L=8):
             "tokens_per_s": round(B / (ms * 1e-3), 0)}
 
 
+STAMP_NAMES = ("entry", "ctx_known", "q_ready", "stream_end", "combine_done", "partials_stored", "counted",
+               "merged")
+
+
+def stamps_config(cx, name, S, L, Hq, Hkv, d, steps, warmup):
+    """Phase timestamps of the decode step kernel (the stamps build: libfriday_attn_stamps.so,
+    the product kernels plus a 100 MHz real-time stamp per phase edge and workgroup). Replays
+    the config's graph, then reads the stamps of the last launch (the last layer of the last
+    replay) and reports, per phase, the spread over the workgroups in us after the earliest
+    entry."""
+    import numpy as np
+
+    fa = cx.fa
+    lib = fa.load()
+    lib.friday_attn_debug_stamps.argtypes = [C.c_void_p]
+    nwg_max = 1 << 14
+    buf = fa.DeviceBuffer(nwg_max * 32 * 8)
+    buf.upload(np.zeros(nwg_max * 32, np.uint64))
+    if lib.friday_attn_debug_stamps(C.c_void_p(buf.ptr)) != 0:
+        raise RuntimeError("friday_attn_debug_stamps failed")
+    dl = DecodeLayers(cx, S, L, Hq, Hkv, d)
+    ms = dl.measure(steps, warmup, "step")
+    dl.free()
+    lib.friday_attn_debug_stamps(None)
+    st = buf.download((nwg_max, 32), np.uint64).astype(np.int64)
+    buf.free()
+    live = st[:, 0] > 0
+    st = st[live]
+    t0 = st[:, 0].min()
+    phases = {}
+    for k, nm in enumerate(STAMP_NAMES):
+        has = st[:, k] > 0
+        if has.any():
+            v = (st[has, k] - t0) / 100.0
+            phases[nm] = {"wgs": int(has.sum()), "min": round(float(v.min()), 2),
+                          "median": round(float(np.median(v)), 2), "max": round(float(v.max()), 2)}
+    tiles = []
+    for i in range(16):
+        has = st[:, 8 + i] > 0
+        if has.any():
+            tiles.append(round(float(np.median((st[has, 8 + i] - t0) / 100.0)), 2))
+    info = st[:, 26]
+    nsp, mk = (info >> 12) & 0xFFF, (info >> 24) - 1
+    xcc = st[:, 24] & 0xF
+    ends = np.where(st[:, 7] > 0, st[:, 7], np.where(st[:, 5] > 0, st[:, 5], st[:, 4]))
+    span = (ends.max() - t0) / 100.0
+    # per-workgroup durations of the phases (median over workgroups)
+    dur = lambda a, b: round(float(np.median((st[:, b] - st[:, a])[(st[:, a] > 0) & (st[:, b] > 0)] / 100.0)), 2)
+    rec = {"config": f"stamps: {name}", "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
+           "us_per_layer_step_stamps_build": round(ms * 1e3 / L, 3), "workgroups": int(live.sum()),
+           "nsp": int(nsp.max()), "launch_span_us": round(span, 2), "phases_us_after_first_entry": phases,
+           "wave0_tile_landed_median_us": tiles,
+           "median_durations_us": {"entry_to_ctx": dur(0, 1), "ctx_to_first_tile": dur(1, 8),
+                                   "entry_to_q_ready": dur(0, 2), "stream_end_to_combine": dur(3, 4),
+                                   "combine_to_partials_stored": dur(4, 5), "partials_to_counted": dur(5, 6),
+                                   "counted_to_merged": dur(6, 7)},
+           "mergers": int((mk >= 0).sum())}
+    # the XCDs each group's workgroups ran on (grid x = the groups, so group = linear id % groups)
+    groups = Hkv * -(-(Hq // Hkv) // 16)
+    lin = np.nonzero(live)[0]
+    rec["xcds_per_group"] = [len(set(xcc[(lin % groups) == g].tolist())) for g in range(groups)]
+    log(f"[bench] stamps {name}: span {span:.2f} us, {json.dumps(phases)}")
+    return rec
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -700,7 +765,7 @@ def main():
                     help="only copy 1 GiB three times with the bench-kit streaming copy (one 16-byte load and "
                          "store per element): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run give the "
                          "counters' reading for a known 1 GiB read + 1 GiB write")
-    ap.add_argument("--config", choices=("headline", "all", "others", "short", "prefill", "paged", "q8", "gemm", "layer", "append"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "short", "prefill", "paged", "q8", "gemm", "layer", "append", "stamps"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other benchmark configs; "
                          "short: configs 1 and 2 only")
     args = ap.parse_args()
@@ -710,6 +775,9 @@ def main():
               f"on a single MI355X; how it would shard is a design note, not a run.", file=sys.stderr)
         sys.exit(2)
 
+    if args.config == "stamps":  # the stamps build of the library, loaded instead of the product one
+        os.environ["FRIDAY_ATTN_LIB"] = os.path.join(ROOT, "friday-inference-engine_amd", "lib",
+                                                     "libfriday_attn_stamps.so")
     cx = Ctx()
     if args.calibrate:
         cx.bk.fabk_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
@@ -771,6 +839,11 @@ def main():
     if args.config == "layer":
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True)), flush=True)
+    if args.config == "stamps":
+        for rec in (stamps_config(cx, "3: 40q/8kv x 64 layers", 32768, 64, 40, 8, 128, args.steps, args.warmup),
+                    stamps_config(cx, "2: 32q/8kv x 32 layers", 1024, 32, 32, 8, 128, args.steps, args.warmup),
+                    stamps_config(cx, "ctx 16, 40q/8kv x 64 layers", 16, 64, 40, 8, 128, args.steps, args.warmup)):
+            print(json.dumps(rec), flush=True)
     if args.config == "gemm":
         for case in GEMM_CASES:
             print(json.dumps(gemm_config(cx, *case, args.steps, args.warmup)), flush=True)

@@ -18,6 +18,9 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libfriday_attn.so")
+# bench-only: the same library with the decode kernels' phase timestamps compiled in
+# (FA_STAMPS=1; bench.py --config stamps), never loaded by the product or the tests
+STAMPS_LIB = os.path.join(LIB_DIR, "libfriday_attn_stamps.so")
 SOURCES = ["fa_api.cpp", "fa_append.hip", "fa_decode.hip", "fa_prefill.hip", "kq_gemm.hip"]
 # benchmark-only helpers (synthetic fill, counter-calibration copy): a separate library
 # next to bench.py, not part of the product
@@ -49,13 +52,13 @@ _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 SOURCE_FLAGS = {"fa_prefill.hip": _VGPR_MFMA, "fa_decode.hip": _VGPR_MFMA, "kq_gemm.hip": _VGPR_MFMA}
 
 
-def _compile(sources, ex):
+def _compile(sources, ex, defines=(), suffix=""):
     objs, jobs = [], []
     for src in sources:
         path = src if os.path.isabs(src) else os.path.join(CSRC, src)
-        obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
+        obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + suffix + ".o")
         objs.append(obj)
-        jobs.append(ex.submit(_run, [HIPCC, *CFLAGS, *SOURCE_FLAGS.get(src, []), "-c", path, "-o", obj]))
+        jobs.append(ex.submit(_run, [HIPCC, *CFLAGS, *SOURCE_FLAGS.get(src, []), *defines, "-c", path, "-o", obj]))
     return objs, jobs
 
 
@@ -71,12 +74,14 @@ def build(verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=8) as ex:
         objs, jobs = _compile(SOURCES, ex)
         bobjs, bjobs = _compile([os.path.abspath(BENCHKIT_SRC)], ex)
-        for j in jobs + bjobs:
+        sobjs, sjobs = _compile(["fa_decode.hip"], ex, ["-DFA_STAMPS=1"], "_stamps")
+        for j in jobs + bjobs + sjobs:
             out = j.result()
             if verbose and out.strip():
                 print(out)
     _link(objs, LIB)
     _link(bobjs, BENCHKIT)
+    _link([o if not o.endswith("fa_decode.o") else sobjs[0] for o in objs], STAMPS_LIB)
     return LIB
 
 

@@ -26,7 +26,40 @@
 #include <type_traits>
 
 namespace fa {
+
+#if FA_STAMPS
+// Phase timestamps of the bench-only stamps build (compiled with FA_STAMPS=1 into a library
+// of its own; the product build has none of this): thread 0 of every decode workgroup writes
+// the 100 MHz real-time counter at each phase edge, with ordinary vector stores, into a
+// host-set buffer of kStampWords 64-bit words per workgroup (workgroup = linear block id).
+__device__ unsigned long long* g_stamps;
+#endif
+
 namespace {
+
+// Stamp slots: 0 entry, 1 context length known, 2 q ready (rotation done), 3 wave 0's
+// stream end, 4 wave combine done, 5 partial stores completed, 6 arrival counted / count
+// observed by a merger, 7 merge stores completed; 8 + i: wave 0's tile i in LDS (i < 16);
+// 24 XCC id, 25 HW_ID, 26 split | nsp << 12 | merger slice + 1 << 24, 27 tiles of the split.
+constexpr int kStampWords = 32;
+__device__ __forceinline__ void stamp_val(int k, unsigned long long v) {
+#if FA_STAMPS
+    if (g_stamps && threadIdx.x == 0) {
+        const size_t wg = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z);
+        g_stamps[wg * kStampWords + k] = v;
+    }
+#else
+    (void)k;
+    (void)v;
+#endif
+}
+__device__ __forceinline__ void stamp(int k) {
+#if FA_STAMPS
+    stamp_val(k, __builtin_amdgcn_s_memrealtime());
+#else
+    (void)k;
+#endif
+}
 
 constexpr int kWaves = 4;  // waves per workgroup (the merge kernel, fp16 and paged decode)
 constexpr int kThreads = kWaves * 64;
@@ -306,6 +339,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     constexpr int NT = W * 64;
     using Gm = Geo<D, Q8, PAGED, W>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
+    stamp(0);
 
     // grid x = (kv head, head block) group, y = split: consecutive workgroup ids walk the
     // groups first, so the dispatch order interleaves groups and, with round-robin
@@ -337,6 +371,10 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     // context length: read once (the device position or sequence length), clamped to the cache
     const int S_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
     const int S = min(S_raw, p.max_seq);
+#if FA_STAMPS
+    asm volatile("" ::"s"(S));
+    stamp(1);
+#endif
     const int chunk = p.single ? (S > 0 ? ((S + kSpan - 1) / kSpan) * kSpan : kSpan)
                                : split_chunk(S, p.min_chunk, p.max_splits);
     const int nsp = p.single ? 1 : split_count(S, p.min_chunk, p.max_splits);
@@ -354,6 +392,16 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
+#if FA_STAMPS
+    {
+        const unsigned xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // HW_REG_XCC_ID[3:0]
+        const unsigned hwid = __builtin_amdgcn_s_getreg((31 << 11) | 4);  // HW_REG_HW_ID
+        stamp_val(24, xcc);
+        stamp_val(25, hwid);
+        stamp_val(26, (unsigned)split | (unsigned)nsp << 12 | (unsigned)(mk + 1) << 24);
+        stamp_val(27, (unsigned)((end - start + kTile - 1) / kTile));
+    }
+#endif
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches on it are scalar
@@ -688,6 +736,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             load_tile(st, t_next);
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
+            if (wave == 0 && t < ntiles && t < 16 * W) stamp(8 + t / W);
         } else {
             if constexpr (PH != 2) {
                 // registers -> wave-private LDS tile (rows past the end are zeros)
@@ -710,6 +759,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             }
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
+            if constexpr (PH != 2) if (wave == 0 && t < ntiles && t < 16 * W) stamp(8 + t / W);
             // Refill this stage while computing. Unconditional, so no branch hides loads from
             // the wait counter (a tile past the end reads nothing and gives zeros).
             if constexpr (PH != 2) load_tile(st, t_next);
@@ -791,6 +841,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             // (With one tile in flight per wave, measured 0.2 us slower at 32k: not used.)
             if (groups > 0) consume(st[0], wave, wave + N * W, std::integral_constant<int, 1>{});
             prepare();
+            stamp(2);
             if (groups > 0) {
                 consume(st[0], wave, wave + N * W, std::integral_constant<int, 2>{});
 #pragma unroll
@@ -805,6 +856,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             }
         } else {
             prepare();
+            stamp(2);
             for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
                 for (int s = 0; s < N; ++s) {
@@ -820,6 +872,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     else
         stream(std::integral_constant<int, NST>{});
 
+    stamp(3);
     // ---- combine the W waves of the workgroup through LDS ----
     // (with a region of its own, each wave writes its state without waiting for the others;
     // over the tiles, every wave must be done reading its tiles first)
@@ -870,6 +923,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         }
     }
 
+    stamp(4);
     // rotated q back into the q buffer once no other workgroup of the group reads it
     auto write_q = [&]() {
         if (ROPE && gvalid) {
@@ -897,14 +951,20 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         // wait until every one of them has completed before this workgroup is counted.
         wait_vmem();
         __syncthreads();
+        stamp(5);
         if (last_arriver) {
             __shared__ int is_last;
             if (tid == 0)
                 is_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - base ==
                           (unsigned)nsp - 1u;
             __syncthreads();
+            stamp(6);
             if (!is_last) return;
             merge_any<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp);
+#if FA_STAMPS
+            wait_vmem();
+            stamp(7);
+#endif
             write_q();  // every workgroup of the group has read q by now
             if (tid == 0) __hip_atomic_store(cnt + kCounterStride / 2, base + (unsigned)nsp, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
@@ -922,8 +982,13 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
+        stamp(6);
         if (gave_up) return;
         merge_slice<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
+#if FA_STAMPS
+        wait_vmem();
+        stamp(7);
+#endif
         if (mk == 0) {
             write_q();  // every workgroup of the group has read q by now
             if (tid == 0) __hip_atomic_store(cnt + kCounterStride / 2, base + (unsigned)nsp, __ATOMIC_RELAXED,
@@ -991,3 +1056,11 @@ int launch_decode(const DecodeParams& p, int head_dim, int batch, bool paged, bo
 }
 
 }  // namespace fa
+
+#if FA_STAMPS
+// Stamps build only: point the decode kernels' phase timestamps at `buf` (device memory of
+// 32 64-bit words per workgroup of the launches that follow; null switches them off).
+extern "C" int friday_attn_debug_stamps(void* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(fa::g_stamps), &buf, sizeof(buf)) == hipSuccess ? 0 : -1;
+}
+#endif
