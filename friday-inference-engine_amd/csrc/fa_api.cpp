@@ -115,6 +115,10 @@ int max_splits() {
     static const int v = env_int("FRIDAY_ATTN_MAX_SPLITS", kMaxSplitsLimit, 1, kMaxSplitsLimit);
     return v;
 }
+int split_major_default() {
+    static const int v = env_int("FRIDAY_ATTN_SPLIT_MAJOR", 0, 0, 1);
+    return v;
+}
 // Compute units of the current device (256 on an MI355X), asked once per device.
 int device_cus() {
     static std::atomic<int> cus[64];

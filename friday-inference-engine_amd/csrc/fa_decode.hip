@@ -355,11 +355,12 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     if (ROPE) { pin_sgpr(p.rope_table); pin_sgpr(p.neox); pin_sgpr(p.k_new); pin_sgpr(p.v_new); }
     // int8 caches: the block scales of one position, for all kv heads, share a cache line, so
     // the workgroups of one split (every kv head group) are placed on one XCD (ids are dealt
-    // to the 8 XCDs in turn) to read those lines through one L2. Within a group the splits
-    // keep increasing with the id, as the fused merge requires.
+    // to the 8 XCDs in turn) to read those lines through one L2; fp16 caches with
+    // split_major set are placed the same way, so that one XCD reads whole cache rows at a
+    // time. Within a group the splits keep increasing with the id, as the fused merge requires.
     int group = blockIdx.x, split = blockIdx.y;
-    if constexpr (Q8 && !PAGED) {
-        if ((gridDim.y & 7) == 0) {
+    if constexpr (!PAGED) {
+        if ((Q8 || p.split_major) && (gridDim.y & 7) == 0) {
             const int lin = blockIdx.x + gridDim.x * blockIdx.y;
             const int r = lin >> 3;
             group = r % gridDim.x;
@@ -1010,6 +1011,7 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
 template <int D, bool PAGED, bool Q8>
 int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
+    p.split_major = split_major_default();
     const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
     // fixed mergers while the whole grid can be resident at once, else the last arriver merges
     const size_t resident = (size_t)device_cus() * wgs_per_cu(PAGED, Q8);

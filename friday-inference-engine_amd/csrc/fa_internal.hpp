@@ -48,6 +48,7 @@ int min_chunk();
 int max_splits();
 int splits_for(int Hkv, int ngb);
 int device_cus();  // compute units of the current device
+int split_major_default();  // FRIDAY_ATTN_SPLIT_MAJOR (0 or 1), read once
 
 struct DecodeParams {
     const uint16_t* q;         // [B][Hq*D]
@@ -79,6 +80,9 @@ struct DecodeParams {
     const uint16_t* k_new;     // [B][kv_dim] raw k of the new token
     const uint16_t* v_new;     // [B][kv_dim] v of the new token
     int neox;
+    // contiguous fp16 caches: 1 deals the workgroups of one split (every group) to one XCD,
+    // as the int8 kernel always does; 0 (default) deals the splits of one group to one XCD
+    int split_major;
 };
 
 int launch_zero_fill(void* ptr, size_t bytes, hipStream_t stream);
