@@ -90,7 +90,8 @@ size_t counters_bytes(int batch, int Hq) { return (size_t)batch * Hq * fa::kCoun
 
 size_t split_ws_bytes(int batch, int Hq, int max_seq, int d) {
     const size_t ns = (size_t)fa::split_bound(max_seq, fa::min_chunk(), fa::max_splits());
-    return counters_bytes(batch, Hq) + (size_t)batch * Hq * ns * ((size_t)d + 2) * sizeof(float);
+    // counter slots, then the partials (o, then m and l), then one flag word per split
+    return counters_bytes(batch, Hq) + (size_t)batch * Hq * ns * ((size_t)d + 3) * sizeof(float);
 }
 
 // counter_region > 0: the partials start at that fixed offset instead of right after this
@@ -100,6 +101,7 @@ void set_workspace(fa::DecodeParams& p, void* ws, int batch, int d, bool fused, 
     p.counters = fused ? reinterpret_cast<int*>(base) : nullptr;
     p.part_o = reinterpret_cast<float*>(base + (counter_region ? counter_region : counters_bytes(batch, p.Hq)));
     p.part_ml = p.part_o + (size_t)batch * p.Hq * p.nsplit_grid * d;
+    p.flags = reinterpret_cast<unsigned*>(p.part_ml + (size_t)batch * p.Hq * p.nsplit_grid * 2);
 }
 
 }  // namespace
@@ -115,9 +117,18 @@ int max_splits() {
     static const int v = env_int("FRIDAY_ATTN_MAX_SPLITS", kMaxSplitsLimit, 1, kMaxSplitsLimit);
     return v;
 }
+// Decode placement and merge form: the environment's choice, read once, until
+// friday_attn_set_decode_form overrides it for the process.
+std::atomic<int> g_local_merge{-1}, g_split_major{-1};
+int local_merge_default() {
+    static const int v = env_int("FRIDAY_ATTN_LOCAL_MERGE", 0, 0, 1);
+    const int o = g_local_merge.load(std::memory_order_relaxed);
+    return o >= 0 ? o : v;
+}
 int split_major_default() {
     static const int v = env_int("FRIDAY_ATTN_SPLIT_MAJOR", 0, 0, 1);
-    return v;
+    const int o = g_split_major.load(std::memory_order_relaxed);
+    return o >= 0 ? o : v;
 }
 // Compute units of the current device (256 on an MI355X), asked once per device.
 int device_cus() {
@@ -287,6 +298,14 @@ int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, v
         return fail(FA_ERR_INVALID, "decode_workspace_init: invalid workspace");
     return launch_status(fa::launch_zero_fill(workspace, workspace_bytes, static_cast<hipStream_t>(stream)),
                          "decode_workspace_init");
+}
+
+int friday_attn_set_decode_form(int local_merge, int split_major) {
+    if (local_merge < -1 || local_merge > 1 || split_major < -1 || split_major > 1)
+        return fail(FA_ERR_INVALID, "set_decode_form: values must be -1, 0 or 1");
+    fa::g_local_merge.store(local_merge, std::memory_order_relaxed);
+    fa::g_split_major.store(split_major, std::memory_order_relaxed);
+    return ok();
 }
 
 int friday_attn_decode_workspace_status(const void* workspace, size_t workspace_bytes, void* stream) {

@@ -166,6 +166,37 @@ __device__ __forceinline__ float2 ld_coherent2(__amdgpu_buffer_rsrc_t r, uint32_
     return *reinterpret_cast<const float2*>(&x);
 }
 
+// The same accesses with the cache policy as a parameter: kCpolSc1 (agent-coherent, as
+// above) or kCpolSc0 (loads miss the CU's L1 and are served by the XCD's L2, coherent with
+// plain stores of other CUs of the same XCD; stores with policy 0 are written to that L2).
+constexpr int kCpolSc0 = 1;
+template <int CP>
+__device__ __forceinline__ f4 ld_pol4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const i4v x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, CP);
+    return *reinterpret_cast<const f4*>(&x);
+}
+template <int CP>
+__device__ __forceinline__ float2 ld_pol2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const i2v x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, 0, CP);
+    return *reinterpret_cast<const float2*>(&x);
+}
+template <int CP>
+__device__ __forceinline__ uint32_t ld_pol1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, CP);
+}
+template <int CP>
+__device__ __forceinline__ void st_pol4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const i4v*>(&v), r, (int)byte_off, 0, CP);
+}
+template <int CP>
+__device__ __forceinline__ void st_pol2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const i2v*>(&v), r, (int)byte_off, 0, CP);
+}
+template <int CP>
+__device__ __forceinline__ void st_pol1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32((int)v, r, (int)byte_off, 0, CP);
+}
+
 // Buffer descriptor from wave-uniform values, built from SGPRs (readfirstlane): without it
 // the compiler may treat the descriptor as divergent and wrap every load in a waterfall loop.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, uint32_t bytes) {

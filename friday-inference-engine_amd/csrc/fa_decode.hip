@@ -220,8 +220,9 @@ __device__ __forceinline__ float max8(float v) {
 // does not depend on the column range or on which workgroup runs it, so the separate
 // merge kernel and the column slices of the fused merge give the same bits. cw must be a
 // power of two; with out_q, cw and c0 must be multiples of 8.
-template <int D, int NT>  // NT: threads of the workgroup
+template <int D, int NT, bool LOCAL = false>  // NT: threads of the workgroup; LOCAL: partials in this XCD's L2
 __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, int c0, int cw) {
+    constexpr int CP = LOCAL ? kCpolSc0 : kCpolSc1;
     constexpr int kUnitsPerPass = NT / 8;
     constexpr int kBatch = 4;  // passes whose partials are loaded in one round trip
     const int tid = threadIdx.x, r = tid & 7;
@@ -245,8 +246,8 @@ __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, 
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t j = (uint32_t)min(r + 8 * i, nsp - 1);
-                ml[k][i] = ld_coherent2(rml, (row + j) * 8);
-                ov[k][i] = ld_coherent4(ro, ((row + j) * D + 4 * (uint32_t)c) * 4);
+                ml[k][i] = ld_pol2<CP>(rml, (row + j) * 8);
+                ov[k][i] = ld_pol4<CP>(ro, ((row + j) * D + 4 * (uint32_t)c) * 4);
             }
         }
 #pragma unroll
@@ -260,7 +261,7 @@ __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, 
 #pragma unroll
             for (int i = 0; i < 4; ++i) M = fmaxf(M, r + 8 * i < nsp ? ml[k][i].x : -__builtin_inff());
             for (int j0 = r + 32; j0 < nsp; j0 += 8)  // beyond 32 splits
-                M = fmaxf(M, ld_coherent2(rml, (row + (uint32_t)j0) * 8).x);
+                M = fmaxf(M, ld_pol2<CP>(rml, (row + (uint32_t)j0) * 8).x);
             M = max8(M);
             float L = 0.0f;
             f4 acc = f4{0.f, 0.f, 0.f, 0.f};
@@ -272,8 +273,8 @@ __device__ void merge_cols(const DecodeParams& p, size_t row0, int nh, int nsp, 
                 acc += w * ov[k][i];
             }
             for (int j0 = r + 32; j0 < nsp; j0 += 8) {
-                const float2 m2 = ld_coherent2(rml, (row + (uint32_t)j0) * 8);
-                const f4 o2 = ld_coherent4(ro, ((row + (uint32_t)j0) * D + 4 * (uint32_t)c) * 4);
+                const float2 m2 = ld_pol2<CP>(rml, (row + (uint32_t)j0) * 8);
+                const f4 o2 = ld_pol4<CP>(ro, ((row + (uint32_t)j0) * D + 4 * (uint32_t)c) * 4);
                 const float df = m2.x - M;
                 const float w = df < kCut2 ? 0.0f : exp2_fast(df);
                 L += w * m2.y;
@@ -298,10 +299,10 @@ __device__ __forceinline__ void merge_any(const DecodeParams& p, size_t row0, in
 }
 
 // Column slice k of nslice of the fused merge.
-template <int D, int NT>
+template <int D, int NT, bool LOCAL = false>
 __device__ __forceinline__ void merge_slice(const DecodeParams& p, size_t row0, int nh, int nsp, int k, int nslice) {
     const int cw = (D / 4) / nslice;
-    merge_cols<D, NT>(p, row0, nh, nsp, k * cw, cw);
+    merge_cols<D, NT, LOCAL>(p, row0, nh, nsp, k * cw, cw);
 }
 
 // Number of column slices the fused merge of a group is spread over: the launcher's
@@ -389,7 +390,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     // (grid x = Hkv * ngb groups)
     unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)b * p.Hkv * p.ngb + group) * kCounterStride;
     unsigned base = 0;
-    if (nsp > 1 && p.counters && (mk >= 0 || last_arriver))
+    if (nsp > 1 && p.counters && (mk >= 0 || last_arriver || p.local_merge))
         base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
@@ -917,10 +918,16 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             for (int i = 0; i < 4; ++i) r[i] = out_half(L > 1e-12f ? O[i] / L : 0.0f);
             store_out4(p, row, D, d4, r);
         } else {
-            // written through to the device coherence point (sc1) for the merging workgroup
+            // written through to the device coherence point (sc1) for the merging workgroup,
+            // or (XCD-local merge) into this XCD's L2, where the mergers of the group read them
             const size_t slot = row * p.nsplit_grid + split;
-            st_coherent4(rpo, (uint32_t)((slot * D + 4 * d4) * 4), O);
-            if (d4 == 0) st_coherent2(rpml, (uint32_t)(slot * 8), float2{M, L});
+            if (p.local_merge) {
+                st_pol4<0>(rpo, (uint32_t)((slot * D + 4 * d4) * 4), O);
+                if (d4 == 0) st_pol2<0>(rpml, (uint32_t)(slot * 8), float2{M, L});
+            } else {
+                st_coherent4(rpo, (uint32_t)((slot * D + 4 * d4) * 4), O);
+                if (d4 == 0) st_coherent2(rpml, (uint32_t)(slot * 8), float2{M, L});
+            }
         }
     }
 
@@ -953,6 +960,58 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         wait_vmem();
         __syncthreads();
         stamp(5);
+        if (p.local_merge) {
+            // XCD-local form (every workgroup of the group runs on one XCD; the launcher sets it
+            // only for fixed mergers and grids whose groups map to one XCD each): the partials
+            // are in this XCD's L2 (completed, above); the split's flag word, also a plain
+            // store, then says so with the launch's tag (the group's target count, base + nsp,
+            // a value no earlier launch on this workspace left there). The mergers poll the
+            // flags with loads that miss the CU's L1 (sc0) and read the partials the same way:
+            // no atomic, and no round trip beyond the XCD's L2.
+            const unsigned target = base + (unsigned)nsp;
+            const size_t frow = ((size_t)b * p.Hkv * p.ngb + group) * p.nsplit_grid;
+            const __amdgpu_buffer_rsrc_t rfl = coherent_rsrc(p.flags + frow, (uint32_t)p.nsplit_grid * 4u);
+            if (tid == 0) st_pol1<0>(rfl, (uint32_t)split * 4u, target);
+            if (mk < 0) return;
+            __shared__ int gave_up_local;
+            if (wave == 0) {
+                // bounded like wait_count; a merger that gives up sets the sticky error bit
+                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                bool done = false;
+                while (true) {
+                    bool ready = true;
+                    for (int j = lane; j < nsp; j += 64) ready = ready && ld_pol1<kCpolSc0>(rfl, (uint32_t)j * 4u) == target;
+                    if (__builtin_amdgcn_ballot_w64(!ready) == 0) {
+                        done = true;
+                        break;
+                    }
+                    if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) break;
+                }
+                if (lane == 0) {
+                    gave_up_local = !done;
+                    if (!done)
+                        __hip_atomic_fetch_or(reinterpret_cast<unsigned*>(p.counters) + kStatusWord, kStatusMergeTimeout,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __syncthreads();
+            stamp(6);
+            if (gave_up_local) return;
+            merge_slice<D, NT, true>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
+#if FA_STAMPS
+            wait_vmem();
+            stamp(7);
+#endif
+            if (mk == 0) {
+                write_q();  // every workgroup of the group has read q by now
+                // counter and base advance together, so the other forms find them equal
+                if (tid == 0) {
+                    __hip_atomic_fetch_add(cnt, (unsigned)nsp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(cnt + kCounterStride / 2, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            return;
+        }
         if (last_arriver) {
             __shared__ int is_last;
             if (tid == 0)
@@ -1016,6 +1075,13 @@ int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
     // fixed mergers while the whole grid can be resident at once, else the last arriver merges
     const size_t resident = (size_t)device_cus() * wgs_per_cu(PAGED, Q8);
     p.merge_slices = (size_t)grid.x * grid.y * grid.z <= resident ? kMergeSlices : 0;
+    // XCD-local merge: fixed mergers, contiguous fp16 caches, groups placed one XCD each
+    // (workgroup ids are dealt to the 8 XCDs in turn, and a group's ids are congruent modulo
+    // the group count, a multiple of 8), and the caller's switch (FRIDAY_ATTN_LOCAL_MERGE)
+    p.local_merge = (!PAGED && !Q8 && !p.single && p.counters && p.flags && p.merge_slices > 0 && !p.split_major &&
+                     grid.x % 8 == 0 && grid.z == 1 && local_merge_default())
+                        ? 1
+                        : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
         hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid,

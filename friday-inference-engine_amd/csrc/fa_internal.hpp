@@ -49,6 +49,7 @@ int max_splits();
 int splits_for(int Hkv, int ngb);
 int device_cus();  // compute units of the current device
 int split_major_default();  // FRIDAY_ATTN_SPLIT_MAJOR (0 or 1), read once
+int local_merge_default();  // FRIDAY_ATTN_LOCAL_MERGE (0 or 1), read once
 
 struct DecodeParams {
     const uint16_t* q;         // [B][Hq*D]
@@ -83,6 +84,10 @@ struct DecodeParams {
     // contiguous fp16 caches: 1 deals the workgroups of one split (every group) to one XCD,
     // as the int8 kernel always does; 0 (default) deals the splits of one group to one XCD
     int split_major;
+    // fused merge, XCD-local form: per-split flag words [B][Hkv*ngb][nsplit_grid] (in the
+    // workspace after the partials) and the launcher's choice of that form
+    unsigned* flags;
+    int local_merge;
 };
 
 int launch_zero_fill(void* ptr, size_t bytes, hipStream_t stream);

@@ -123,6 +123,17 @@ int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, v
  * friday_attn_decode_workspace_init clears it. Covers every call that takes a workspace
  * (fused, step, int8 step, quant step, paged). */
 int friday_attn_decode_workspace_status(const void* workspace, size_t workspace_bytes, void* stream);
+/* No counterpart in the reference (a tuning switch of this implementation). Chooses, for
+ * the whole process, how later fp16 contiguous decode launches place their workgroups and
+ * merge their splits; results are bit-identical in every form. local_merge = 1: when the
+ * fixed mergers serve the launch and every (kv head, head block) group maps to one XCD
+ * (the group count a multiple of 8), the splits hand their partials to the mergers through
+ * that XCD's L2 (flag words in the workspace) instead of through device-coherent memory.
+ * split_major = 1: the workgroups of one split (all groups) are dealt to one XCD, as the
+ * int8 kernel does (this excludes local_merge). -1 restores the environment's choice
+ * (FRIDAY_ATTN_LOCAL_MERGE, FRIDAY_ATTN_SPLIT_MAJOR; default 0). Not for use while
+ * launches are being recorded into a graph that must keep the earlier form. */
+int friday_attn_set_decode_form(int local_merge, int split_major);
 /* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
  * few workgroups of each kv head (the ones dispatched last), each over a slice of the
  * columns, once an arrival counter in the workspace shows every split stored, instead

@@ -231,3 +231,10 @@ def test_decode_alignment_and_status_checks(fa):
     # the status query needs a workspace that holds counter slot 0
     assert L.friday_attn_decode_workspace_status(None, 4096, None) == fa.FA_ERR_INVALID
     assert L.friday_attn_decode_workspace_status(FAKE, 16, None) == fa.FA_ERR_INVALID
+
+
+def test_set_decode_form_rejects_bad_values(fa):
+    L = fa.load()
+    assert L.friday_attn_set_decode_form(2, 0) == fa.FA_ERR_INVALID
+    assert L.friday_attn_set_decode_form(0, -2) == fa.FA_ERR_INVALID
+    assert L.friday_attn_set_decode_form(-1, -1) == fa.FA_OK
