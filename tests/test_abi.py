@@ -59,6 +59,10 @@ def test_split_workspace_rules(fa):
     L = fa.load()
     need = L.friday_attn_split_workspace_bytes(40, 32768)
     assert need > 0 and L.friday_attn_split_workspace_bytes(0, 10) == 0
+    # layout: a 256-byte counter slot per query head, then per (head, split) d = 128 partial
+    # values, (max, sum) and one flag word; at most 128 splits of >= 128 positions
+    assert need == 40 * 256 + 40 * 128 * (128 + 3) * 4
+    assert L.friday_attn_split_workspace_bytes(40, 1000) == 40 * 256 + 40 * 8 * (128 + 3) * 4
     # too small a workspace is refused before any launch
     rc = L.friday_attn_decode_attention_split(FAKE, FAKE, FAKE, FAKE, 32768, None, 32768, 40, 8, 128, FAKE, need // 2,
                                               None, None, None)
