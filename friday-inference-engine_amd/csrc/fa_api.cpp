@@ -119,7 +119,13 @@ int max_splits() {
 }
 // Decode placement and merge form: the environment's choice, read once, until
 // friday_attn_set_decode_form overrides it for the process.
-std::atomic<int> g_local_merge{-1}, g_split_major{-1};
+std::atomic<int> g_local_merge{-1}, g_split_major{-1}, g_kv_pair{-1};
+int kv_pair_for(bool paged, int Hkv, int ngb) {
+    static const int v = env_int("FRIDAY_ATTN_KV_PAIR", 0, 0, 1);
+    const int o = g_kv_pair.load(std::memory_order_relaxed);
+    const int want = o >= 0 ? o : v;
+    return want && !paged && ngb == 1 && Hkv % 2 == 0 ? 2 : 1;
+}
 int local_merge_default() {
     static const int v = env_int("FRIDAY_ATTN_LOCAL_MERGE", 0, 0, 1);
     const int o = g_local_merge.load(std::memory_order_relaxed);
@@ -246,7 +252,8 @@ static int decode_common(const char* w, const uint16_t* q, const void* k, const 
     p.out = out; p.Hq = Hq; p.Hkv = Hkv; p.G = G; p.ngb = (G + 15) / 16; p.kv_dim = Hkv * d;
     p.single = single ? 1 : 0;
     p.min_chunk = fa::min_chunk();
-    p.max_splits = fa::splits_for(Hkv, p.ngb);
+    p.kpw = fa::kv_pair_for(false, Hkv, p.ngb);
+    p.max_splits = fa::splits_for(Hkv / p.kpw, p.ngb);
     p.scale2 = (1.0f / std::sqrt((float)d)) * 1.4426950408889634f;
     if (!single) {
         // host length: the grid only needs the splits of seq_len
@@ -300,11 +307,12 @@ int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, v
                          "decode_workspace_init");
 }
 
-int friday_attn_set_decode_form(int local_merge, int split_major) {
-    if (local_merge < -1 || local_merge > 1 || split_major < -1 || split_major > 1)
+int friday_attn_set_decode_form(int local_merge, int split_major, int kv_pair) {
+    if (local_merge < -1 || local_merge > 1 || split_major < -1 || split_major > 1 || kv_pair < -1 || kv_pair > 1)
         return fail(FA_ERR_INVALID, "set_decode_form: values must be -1, 0 or 1");
     fa::g_local_merge.store(local_merge, std::memory_order_relaxed);
     fa::g_split_major.store(split_major, std::memory_order_relaxed);
+    fa::g_kv_pair.store(kv_pair, std::memory_order_relaxed);
     return ok();
 }
 
@@ -357,7 +365,8 @@ int decode_step_common(const char* w, uint16_t* q, const uint16_t* k, const uint
     p.out_q = out_q; p.out_d = out_d;
     p.kv_dim = num_kv_heads * head_dim;
     p.min_chunk = fa::min_chunk();
-    p.max_splits = fa::splits_for(num_kv_heads, p.ngb);
+    p.kpw = fa::kv_pair_for(false, num_kv_heads, p.ngb);
+    p.max_splits = fa::splits_for(num_kv_heads / p.kpw, p.ngb);
     p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
     p.rope_table = rope_table; p.k_new = k; p.v_new = v; p.neox = neox ? 1 : 0;
     const int grid_len = d_pos ? max_ctx : pos + 1;
@@ -526,6 +535,7 @@ static int paged_decode_common(const char* w, uint16_t* q, const uint16_t* k_new
     p.scale2 = (1.0f / std::sqrt((float)head_dim)) * 1.4426950408889634f;
     p.rope_table = rope_table; p.k_new = k_new; p.v_new = v_new; p.neox = neox ? 1 : 0;
     p.min_chunk = fa::min_chunk();
+    p.kpw = 1;
     p.max_splits = fa::splits_for(num_kv_heads, p.ngb);
     p.nsplit_grid = fa::split_bound(max_seq_len, p.min_chunk, p.max_splits);
     const size_t need = split_ws_bytes(batch, num_heads, max_seq_len, head_dim);

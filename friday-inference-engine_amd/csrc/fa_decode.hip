@@ -71,8 +71,8 @@ constexpr int kStages = 1;    // register stages (tiles in flight) per wave
 // SIMD, one workgroup per CU) let one wave's issue overlap the other's wait.
 constexpr int kWavesQ8 = 8;
 constexpr int kStagesQ8 = 1;
-// waves per workgroup of a decode kernel
-constexpr int waves_for(bool paged, bool q8) { return q8 && !paged ? kWavesQ8 : kWaves; }
+// waves per workgroup of a decode kernel; KPW = 2: two kv heads per workgroup, four waves each
+constexpr int waves_for(bool paged, bool q8, int kpw = 1) { return kpw == 2 ? 2 * kWaves : (q8 && !paged ? kWavesQ8 : kWaves); }
 constexpr int kShortStages = 4;  // stages when a wave has at most this many tiles
 // Paged grids hold several workgroups per CU: three per CU (at most 168 registers), and at
 // most two tiles in flight per wave in the short-split form, where four made the waves of a
@@ -332,11 +332,19 @@ __device__ __forceinline__ bool wait_count(const unsigned* cnt, unsigned target)
 
 // Workgroups per CU the register budget is set for: fp16 two (two waves per SIMD, up to 256
 // registers), paged three (up to 168), contiguous int8 one of eight waves (two per SIMD).
-constexpr int wgs_per_cu(bool paged, bool q8) { return paged ? kPagedWgsPerCu : (q8 ? 1 : 2); }
+// Two kv heads per workgroup (eight waves): one.
+constexpr int wgs_per_cu(bool paged, bool q8, int kpw = 1) { return kpw == 2 ? 1 : (paged ? kPagedWgsPerCu : (q8 ? 1 : 2)); }
 
-template <int D, bool PAGED, bool Q8, int NST, bool ROPE>
-__global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) void fa_decode_kernel(DecodeParams p) {
-    constexpr int W = waves_for(PAGED, Q8);  // waves of this workgroup
+// KPW: kv heads per workgroup. 1: the grid's x walks (kv head, head block) groups and all W
+// waves take interleaved tiles of one kv head's split. 2 (contiguous caches, G <= 16): x
+// walks kv-head pairs, waves [0, 4) take kv head 2x and waves [4, 8) kv head 2x + 1 over the
+// same positions, so a workgroup reads twice the bytes of each cache row (two adjacent
+// kv-head slices); the pair is the merge group.
+template <int D, bool PAGED, bool Q8, int NST, bool ROPE, int KPW>
+__global__ __launch_bounds__(waves_for(PAGED, Q8, KPW) * 64, wgs_per_cu(PAGED, Q8, KPW)) void fa_decode_kernel(DecodeParams p) {
+    static_assert(KPW == 1 || (KPW == 2 && !PAGED), "kv-head pairs: contiguous caches");
+    constexpr int W = waves_for(PAGED, Q8, KPW);  // waves of this workgroup
+    constexpr int WT = W / KPW;                    // waves per kv head (tile interleave)
     constexpr int NT = W * 64;
     using Gm = Geo<D, Q8, PAGED, W>;
     __shared__ __align__(16) unsigned char smem[Gm::LDS];
@@ -368,7 +376,12 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             split = (lin & 7) + 8 * (r / gridDim.x);
         }
     }
-    const int kvh = group / p.ngb, gb = group % p.ngb;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches on it are scalar
+    const int half = KPW == 2 ? wave / WT : 0;                  // this wave's kv head of the pair
+    const int wt = KPW == 2 ? wave % WT : wave;                 // its place in the head's tile interleave
+    const int kvh = (group / p.ngb) * KPW + half, gb = group % p.ngb;
+    const int ngroups = p.Hkv / KPW * p.ngb;                    // grid x
     const int b = blockIdx.z;
     // context length: read once (the device position or sequence length), clamped to the cache
     const int S_raw = PAGED ? p.seq_lens[b] : (p.d_pos ? *p.d_pos + 1 : p.seq_len);
@@ -388,7 +401,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     const int nslice = (nsp > 1 && p.counters && !last_arriver) ? merge_slices<D>(p, nsp) : 1;
     const int mk = split - (nsp - nslice);
     // (grid x = Hkv * ngb groups)
-    unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)b * p.Hkv * p.ngb + group) * kCounterStride;
+    unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)b * ngroups + group) * kCounterStride;
     unsigned base = 0;
     if (nsp > 1 && p.counters && (mk >= 0 || last_arriver || p.local_merge))
         base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -405,8 +418,6 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     }
 #endif
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: branches on it are scalar
     const int col = lane & 15, kb = lane >> 4;
     const int g = gb * 16 + col;
     const bool gvalid = g < p.G;
@@ -438,7 +449,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     float2 rcs[PPT];
     h8 nk[NH], nkp[NH], nv[NH];
     float2 ncs[ROPE ? CW : 1];
-    int append_wave = -1, append_tile = -1, append_row = -1;
+    int append_wt = -1, append_tile = -1, append_row = -1;  // per kv head: its wave wt == append_wt
     // q is rotated only when position S-1 is the new token's own position inside the cache,
     // as the separate append does (it skips positions < 0 and >= max_ctx)
     bool rot_q = false;
@@ -449,7 +460,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         rot_q = S > 0 && S_raw == S;
         if (rot_q && split == nsp - 1) {
             const int last_tile = (end - start - 1) / kTile;
-            append_wave = last_tile % W;
+            append_wt = last_tile % WT;
             append_tile = last_tile;
             append_row = (S - 1) - (start + last_tile * kTile);
         }
@@ -501,7 +512,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             }
         }
         // only the append wave needs the new row chunk (and its rotation partner) of its lane
-        if (wave == append_wave) {
+        if (wt == append_wt) {
             const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
             const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
 #pragma unroll
@@ -569,7 +580,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
 #pragma unroll
                 for (int s = 0; s < Gm::KSTEPS; ++s) qf[s] = *reinterpret_cast<const h8*>(qx + col * D + s * 32 + kb * 8);
             }
-            if (wave == append_wave) {
+            if (wt == append_wt) {
                 h8 r[NH];
 #pragma unroll
                 for (int i = 0; i < NH; ++i) {
@@ -657,7 +668,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     static_assert(kTile == kPageTokens, "one page per tile");
     int wpages = 0;
     if constexpr (PAGED) {
-        const int pt = start + (wave + W * lane) * kTile;
+        const int pt = start + (wt + WT * lane) * kTile;
         wpages = pt < end ? p.block_table[(size_t)b * p.bt_stride + (pt >> 4)] : 0;
     }
     const uint32_t lane_off = (uint32_t)(lrow * rowb + lchunk * 16);
@@ -668,7 +679,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         const uint32_t nrows = (uint32_t)min(max(end - base, 0), kTile);
         size_t row0 = (size_t)base;  // cache row of the tile's first position
         if constexpr (PAGED) {
-            const int li = (t - wave) / W;  // this wave's tile number (uniform)
+            const int li = (t - wt) / WT;  // this wave's tile number (uniform)
             int phys;
             if (li < 64)
                 phys = __builtin_amdgcn_readlane(wpages, li);
@@ -717,7 +728,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
                 sv[r] = __builtin_bit_cast(_Float16, st.vs[r]);
                 // the new row, as quantized and written to the cache by this wave (selects on
                 // the raw codes: cheaper here than rewriting the dequantised row afterwards)
-                if (ROPE && t == append_tile && wave == append_wave && row == append_row) {
+                if (ROPE && t == append_tile && wt == append_wt && row == append_row) {
                     ck[r] = kq;
                     cv[r] = vq;
                     sk[r] = (_Float16)ksc;  // fp16 values: exact
@@ -738,7 +749,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             load_tile(st, t_next);
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
-            if (wave == 0 && t < ntiles && t < 16 * W) stamp(8 + t / W);
+            if (wave == 0 && t < ntiles && t < 16 * WT) stamp(8 + t / WT);
         } else {
             if constexpr (PH != 2) {
                 // registers -> wave-private LDS tile (rows past the end are zeros)
@@ -752,7 +763,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             if constexpr (PH != 1) {
                 // the new row, as written to the cache by this wave, over the one loaded (a
                 // wave's LDS writes complete in order); one tile of one wave
-                if (ROPE && t == append_tile && wave == append_wave) {
+                if (ROPE && t == append_tile && wt == append_wt) {
                     if (lrow == append_row % Gm::RPI) {
                         *reinterpret_cast<u4*>(kl + append_row * Gm::LROW + lchunk * 16) = rk;
                         *reinterpret_cast<u4*>(vl + append_row * Gm::LROW + lchunk * 16) = *reinterpret_cast<const u4*>(&nv[0]);
@@ -761,7 +772,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             }
             // LDS operations of one wave complete in order: the reads below see these writes.
             __builtin_amdgcn_wave_barrier();
-            if constexpr (PH != 2) if (wave == 0 && t < ntiles && t < 16 * W) stamp(8 + t / W);
+            if constexpr (PH != 2) if (wave == 0 && t < ntiles && t < 16 * WT) stamp(8 + t / WT);
             // Refill this stage while computing. Unconditional, so no branch hides loads from
             // the wait counter (a tile past the end reads nothing and gives zeros).
             if constexpr (PH != 2) load_tile(st, t_next);
@@ -824,7 +835,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     // uniform trip count: groups of N tiles of this wave (tiles wave, wave + W, ...).
     // Long splits keep one tile in flight per wave (more congests HBM); short ones, whose
     // waves have at most four tiles, issue them all at once (one memory latency).
-    const int my_tiles = ntiles > wave ? (ntiles - wave + W - 1) / W : 0;
+    const int my_tiles = ntiles > wt ? (ntiles - wt + WT - 1) / WT : 0;
     auto stream = [&](auto n_tag) {
         constexpr int N = decltype(n_tag)::value;
         Stage st[N];
@@ -832,7 +843,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         if (ROPE) load_inputs();
         if (groups > 0) {
 #pragma unroll
-            for (int s = 0; s < N; ++s) load_tile(st[s], wave + s * W);
+            for (int s = 0; s < N; ++s) load_tile(st[s], wt + s * WT);
         }
         if (!ROPE) load_inputs();
         using Whole = std::integral_constant<int, 0>;
@@ -841,19 +852,19 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             // LDS, and its stage's refill is issued, before the q rotation (whose loads and
             // barrier it would otherwise wait behind); its QK then waits for the rotated q.
             // (With one tile in flight per wave, measured 0.2 us slower at 32k: not used.)
-            if (groups > 0) consume(st[0], wave, wave + N * W, std::integral_constant<int, 1>{});
+            if (groups > 0) consume(st[0], wt, wt + N * WT, std::integral_constant<int, 1>{});
             prepare();
             stamp(2);
             if (groups > 0) {
-                consume(st[0], wave, wave + N * W, std::integral_constant<int, 2>{});
+                consume(st[0], wt, wt + N * WT, std::integral_constant<int, 2>{});
 #pragma unroll
-                for (int s = 1; s < N; ++s) consume(st[s], wave + s * W, wave + (N + s) * W, Whole{});
+                for (int s = 1; s < N; ++s) consume(st[s], wt + s * WT, wt + (N + s) * WT, Whole{});
             }
             for (int gi = 1; gi < groups; ++gi) {
 #pragma unroll
                 for (int s = 0; s < N; ++s) {
-                    const int ts = wave + (gi * N + s) * W;
-                    consume(st[s], ts, ts + N * W, Whole{});
+                    const int ts = wt + (gi * N + s) * WT;
+                    consume(st[s], ts, ts + N * WT, Whole{});
                 }
             }
         } else {
@@ -862,14 +873,14 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             for (int gi = 0; gi < groups; ++gi) {
 #pragma unroll
                 for (int s = 0; s < N; ++s) {
-                    const int ts = wave + (gi * N + s) * W;
-                    consume(st[s], ts, ts + N * W, Whole{});
+                    const int ts = wt + (gi * N + s) * WT;
+                    consume(st[s], ts, ts + N * WT, Whole{});
                 }
             }
         }
     };
     constexpr int kShort = PAGED ? kShortStagesPaged : kShortStages;
-    if ((ntiles + W - 1) / W <= kShort)
+    if ((ntiles + WT - 1) / WT <= kShort)
         stream(std::integral_constant<int, kShort>{});
     else
         stream(std::integral_constant<int, NST>{});
@@ -896,21 +907,28 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     const int gcount = min(16, p.G - gb * 16);
     const __amdgpu_buffer_rsrc_t rpo = coherent_rsrc(p.part_o, 0x7fffffff);
     const __amdgpu_buffer_rsrc_t rpml = coherent_rsrc(p.part_ml, 0x7fffffff);
-    for (int idx = tid; idx < gcount * (D / 4); idx += NT) {
-        const int gg = idx / (D / 4), d4 = idx % (D / 4);
-        float M = cm[gg];
+    // (KPW = 2: the first half of the index range is kv head 2x with waves [0, WT), the
+    // second kv head 2x + 1 with waves [WT, 2 WT))
+    for (int idx = tid; idx < KPW * gcount * (D / 4); idx += NT) {
+        const int hf = KPW == 2 ? idx / (gcount * (D / 4)) : 0;
+        const int rem = idx - hf * gcount * (D / 4);
+        const int gg = rem / (D / 4), d4 = rem % (D / 4);
+        const float* hm = cm + hf * WT * 16;
+        const float* hl = cl + hf * WT * 16;
+        const float* ho = co + hf * WT * 16 * Gm::CROW;
+        float M = hm[gg];
 #pragma unroll
-        for (int w = 1; w < W; ++w) M = fmaxf(M, cm[w * 16 + gg]);
+        for (int w = 1; w < WT; ++w) M = fmaxf(M, hm[w * 16 + gg]);
         float L = 0.0f;
         f4 O = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const float df = cm[w * 16 + gg] - M;
-            const float wt = df < kCut2 ? 0.0f : exp2_fast(df);
-            L += wt * cl[w * 16 + gg];
-            O += wt * *reinterpret_cast<const f4*>(co + (w * 16 + gg) * Gm::CROW + 4 * d4);
+        for (int w = 0; w < WT; ++w) {
+            const float df = hm[w * 16 + gg] - M;
+            const float wgt = df < kCut2 ? 0.0f : exp2_fast(df);
+            L += wgt * hl[w * 16 + gg];
+            O += wgt * *reinterpret_cast<const f4*>(ho + (w * 16 + gg) * Gm::CROW + 4 * d4);
         }
-        const int hh = kvh * p.G + gb * 16 + gg;
+        const int hh = ((group / p.ngb) * KPW + hf) * p.G + gb * 16 + gg;
         const size_t row = (size_t)b * p.Hq + hh;
         if (nsp == 1) {
             h4 r;
@@ -932,6 +950,9 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
     }
 
     stamp(4);
+    // the merge group's head rows: one kv head's head block, or (KPW = 2) both heads of the pair
+    const size_t mrow0 = (size_t)b * p.Hq + (size_t)(group / p.ngb) * KPW * p.G + gb * 16;
+    const int mrows = KPW == 2 ? 2 * p.G : gcount;
     // rotated q back into the q buffer once no other workgroup of the group reads it
     auto write_q = [&]() {
         if (ROPE && gvalid) {
@@ -969,7 +990,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             // flags with loads that miss the CU's L1 (sc0) and read the partials the same way:
             // no atomic, and no round trip beyond the XCD's L2.
             const unsigned target = base + (unsigned)nsp;
-            const size_t frow = ((size_t)b * p.Hkv * p.ngb + group) * p.nsplit_grid;
+            const size_t frow = ((size_t)b * ngroups + group) * p.nsplit_grid;
             const __amdgpu_buffer_rsrc_t rfl = coherent_rsrc(p.flags + frow, (uint32_t)p.nsplit_grid * 4u);
             if (tid == 0) st_pol1<0>(rfl, (uint32_t)split * 4u, target);
             if (mk < 0) return;
@@ -997,7 +1018,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             __syncthreads();
             stamp(6);
             if (gave_up_local) return;
-            merge_slice<D, NT, true>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
+            merge_slice<D, NT, true>(p, mrow0, mrows, nsp, mk, nslice);
 #if FA_STAMPS
             wait_vmem();
             stamp(7);
@@ -1020,7 +1041,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
             __syncthreads();
             stamp(6);
             if (!is_last) return;
-            merge_any<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp);
+            merge_any<D, NT>(p, mrow0, mrows, nsp);
 #if FA_STAMPS
             wait_vmem();
             stamp(7);
@@ -1044,7 +1065,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8) * 64, wgs_per_cu(PAGED, Q8)) v
         __syncthreads();
         stamp(6);
         if (gave_up) return;
-        merge_slice<D, NT>(p, (size_t)b * p.Hq + kvh * p.G + gb * 16, gcount, nsp, mk, nslice);
+        merge_slice<D, NT>(p, mrow0, mrows, nsp, mk, nslice);
 #if FA_STAMPS
         wait_vmem();
         stamp(7);
@@ -1067,13 +1088,14 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
     merge_any<D, kThreads>(p, (size_t)row, 1, nsp);
 }
 
-template <int D, bool PAGED, bool Q8>
-int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
+template <int D, bool PAGED, bool Q8, int KPW>
+int launch_k(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
     p.split_major = split_major_default();
-    const dim3 grid(p.Hkv * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
+    const dim3 grid(p.Hkv / KPW * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
+    const dim3 block(waves_for(PAGED, Q8, KPW) * 64);
     // fixed mergers while the whole grid can be resident at once, else the last arriver merges
-    const size_t resident = (size_t)device_cus() * wgs_per_cu(PAGED, Q8);
+    const size_t resident = (size_t)device_cus() * wgs_per_cu(PAGED, Q8, KPW);
     p.merge_slices = (size_t)grid.x * grid.y * grid.z <= resident ? kMergeSlices : 0;
     // XCD-local merge: fixed mergers, contiguous fp16 caches, groups placed one XCD each
     // (workgroup ids are dealt to the 8 XCDs in turn, and a group's ids are congruent modulo
@@ -1084,18 +1106,31 @@ int launch_t(const DecodeParams& p_in, int batch, hipStream_t stream) {
                         : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
-        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true>), grid,
-                           dim3(waves_for(PAGED, Q8) * 64), 0, stream, p);
+        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true, KPW>), grid, block, 0,
+                           stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, false>), grid,
-                       dim3(waves_for(PAGED, Q8) * 64), 0, stream, p);
+    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, false, KPW>), grid, block, 0, stream,
+                       p);
     if (hipGetLastError() != hipSuccess) return -1;
     if (!p.single && !p.counters) {
         hipLaunchKernelGGL((fa_merge_kernel<D, PAGED>), dim3(batch * p.Hq), dim3(kThreads), 0, stream, p);
         if (hipGetLastError() != hipSuccess) return -1;
     }
     return 0;
+}
+
+// kv heads per workgroup: the host's choice (DecodeParams::kpw, which also set the split
+// bound); pairs only for contiguous caches with one head block per kv head
+template <int D, bool PAGED, bool Q8>
+int launch_t(const DecodeParams& p, int batch, hipStream_t stream) {
+    if constexpr (!PAGED) {
+        if (p.kpw == 2) {
+            if (p.ngb != 1 || p.Hkv % 2) return -2;
+            return launch_k<D, PAGED, Q8, 2>(p, batch, stream);
+        }
+    }
+    return launch_k<D, PAGED, Q8, 1>(p, batch, stream);
 }
 
 __global__ void fa_zero_kernel(uint32_t* p, size_t n) {

@@ -50,6 +50,7 @@ int splits_for(int Hkv, int ngb);
 int device_cus();  // compute units of the current device
 int split_major_default();  // FRIDAY_ATTN_SPLIT_MAJOR (0 or 1), read once
 int local_merge_default();  // FRIDAY_ATTN_LOCAL_MERGE (0 or 1), read once
+int kv_pair_for(bool paged, int Hkv, int ngb);  // kv heads per decode workgroup (FRIDAY_ATTN_KV_PAIR)
 
 struct DecodeParams {
     const uint16_t* q;         // [B][Hq*D]
@@ -88,6 +89,9 @@ struct DecodeParams {
     // workspace after the partials) and the launcher's choice of that form
     unsigned* flags;
     int local_merge;
+    // kv heads per workgroup (1, or 2 for contiguous caches with G <= 16): set by the host
+    // together with the split bound it implies (splits_for over Hkv / kpw groups)
+    int kpw;
 };
 
 int launch_zero_fill(void* ptr, size_t bytes, hipStream_t stream);

@@ -46,7 +46,7 @@ API = [
     ("friday_attn_decode_attention_split", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     ("friday_attn_decode_workspace_init", _I, [_P, _SZ, _P]),
     ("friday_attn_decode_workspace_status", _I, [_P, _SZ, _P]),
-    ("friday_attn_set_decode_form", _I, [_I, _I]),
+    ("friday_attn_set_decode_form", _I, [_I, _I, _I]),
     ("friday_attn_decode_attention_fused", _I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     ("friday_attn_decode_step", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _SZ, _P]),
     ("friday_attn_decode_step_noalloc", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P]),
@@ -430,10 +430,11 @@ def decodeWorkspaceInit(workspace, workspace_bytes=None, stream=None):
     _check(load().friday_attn_decode_workspace_init(_ptr(workspace), workspace_bytes, stream))
 
 
-def setDecodeForm(local_merge: int = -1, split_major: int = -1) -> None:
+def setDecodeForm(local_merge: int = -1, split_major: int = -1, kv_pair: int = -1) -> None:
     """friday_attn_set_decode_form: process-wide decode placement / merge form (-1: the
-    environment's choice). Results are bit-identical in every form."""
-    _check(load().friday_attn_set_decode_form(local_merge, split_major))
+    environment's choice). local_merge and split_major give bit-identical results; kv_pair
+    changes the split bound (results within the decode tolerance)."""
+    _check(load().friday_attn_set_decode_form(local_merge, split_major, kv_pair))
 
 
 def decodeWorkspaceStatus(workspace, workspace_bytes=None, stream=None) -> int:

@@ -124,16 +124,21 @@ int friday_attn_decode_workspace_init(void* workspace, size_t workspace_bytes, v
  * (fused, step, int8 step, quant step, paged). */
 int friday_attn_decode_workspace_status(const void* workspace, size_t workspace_bytes, void* stream);
 /* No counterpart in the reference (a tuning switch of this implementation). Chooses, for
- * the whole process, how later fp16 contiguous decode launches place their workgroups and
- * merge their splits; results are bit-identical in every form. local_merge = 1: when the
- * fixed mergers serve the launch and every (kv head, head block) group maps to one XCD
- * (the group count a multiple of 8), the splits hand their partials to the mergers through
- * that XCD's L2 (flag words in the workspace) instead of through device-coherent memory.
- * split_major = 1: the workgroups of one split (all groups) are dealt to one XCD, as the
- * int8 kernel does (this excludes local_merge). -1 restores the environment's choice
- * (FRIDAY_ATTN_LOCAL_MERGE, FRIDAY_ATTN_SPLIT_MAJOR; default 0). Not for use while
- * launches are being recorded into a graph that must keep the earlier form. */
-int friday_attn_set_decode_form(int local_merge, int split_major);
+ * the whole process, how later contiguous decode launches place their workgroups and merge
+ * their splits. local_merge = 1 (fp16 caches): when the fixed mergers serve the launch and
+ * every (kv head, head block) group maps to one XCD (the group count a multiple of 8), the
+ * splits hand their partials to the mergers through that XCD's L2 (flag words in the
+ * workspace) instead of through device-coherent memory; results are bit-identical.
+ * split_major = 1 (fp16 caches): the workgroups of one split (all groups) are dealt to one
+ * XCD, as the int8 kernel always does (this excludes local_merge); bit-identical.
+ * kv_pair = 1 (fp16 and int8 caches, G <= 16, an even kv head count): a workgroup serves two
+ * adjacent kv heads (four waves each), so it reads two adjacent kv-head slices of every
+ * cache row; the split bound follows the halved group count, so results agree with the
+ * other forms within the decode tolerance, not bit for bit. -1 restores the environment's
+ * choice (FRIDAY_ATTN_LOCAL_MERGE, FRIDAY_ATTN_SPLIT_MAJOR, FRIDAY_ATTN_KV_PAIR; default 0).
+ * Paged launches keep one kv head per workgroup and the counter merge. A captured launch
+ * keeps the form it was recorded with. */
+int friday_attn_set_decode_form(int local_merge, int split_major, int kv_pair);
 /* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
  * few workgroups of each kv head (the ones dispatched last), each over a slice of the
  * columns, once an arrival counter in the workspace shows every split stored, instead

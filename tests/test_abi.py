@@ -239,6 +239,7 @@ def test_decode_alignment_and_status_checks(fa):
 
 def test_set_decode_form_rejects_bad_values(fa):
     L = fa.load()
-    assert L.friday_attn_set_decode_form(2, 0) == fa.FA_ERR_INVALID
-    assert L.friday_attn_set_decode_form(0, -2) == fa.FA_ERR_INVALID
-    assert L.friday_attn_set_decode_form(-1, -1) == fa.FA_OK
+    assert L.friday_attn_set_decode_form(2, 0, 0) == fa.FA_ERR_INVALID
+    assert L.friday_attn_set_decode_form(0, -2, 0) == fa.FA_ERR_INVALID
+    assert L.friday_attn_set_decode_form(0, 0, 3) == fa.FA_ERR_INVALID
+    assert L.friday_attn_set_decode_form(-1, -1, -1) == fa.FA_OK

@@ -21,7 +21,7 @@ FORMS = ((0, 0), (1, 0), (0, 1))  # (local_merge, split_major)
 @pytest.fixture
 def forms(gpu):
     yield gpu
-    gpu.setDecodeForm(-1, -1)
+    gpu.setDecodeForm(-1, -1, -1)
 
 
 def fused(fa, q, kc, vc, S, Hq, Hkv, d, max_ctx, ws, pos):
@@ -47,7 +47,7 @@ def test_fused_forms_identical(forms, Hq, Hkv, d):
     pos = fa.DeviceBuffer(4)
     lengths = (8192, 8192, 300, 4097, 129, 8000, 8000)
     want = {}
-    fa.setDecodeForm(0, 0)
+    fa.setDecodeForm(0, 0, 0)
     ws0 = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_ctx))
     fa.decodeWorkspaceInit(ws0)
     for S in set(lengths):
@@ -55,7 +55,7 @@ def test_fused_forms_identical(forms, Hq, Hkv, d):
     shared = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_ctx))
     fa.decodeWorkspaceInit(shared)
     for form in FORMS:
-        fa.setDecodeForm(*form)
+        fa.setDecodeForm(*form, 0)
         own = fa.DeviceBuffer(fa.splitAttentionWorkspaceBytes(Hq, max_ctx))
         fa.decodeWorkspaceInit(own)
         print(f"[forms] fused {Hq}q/{Hkv}kv d{d} form {form}", flush=True)
@@ -89,7 +89,7 @@ def test_step_forms_identical(forms):
     for S in (32768, 5000):
         for form in FORMS:
             print(f"[forms] step S={S} form {form}", flush=True)
-            fa.setDecodeForm(*form)
+            fa.setDecodeForm(*form, 0)
             for n, a in host.items():
                 b[n].upload(a)
             dpos.upload(np.array([S - 1], np.int32))
