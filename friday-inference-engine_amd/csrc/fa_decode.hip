@@ -939,7 +939,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8, KPW) * 64, wgs_per_cu(PAGED, Q
             // written through to the device coherence point (sc1) for the merging workgroup,
             // or (XCD-local merge) into this XCD's L2, where the mergers of the group read them
             const size_t slot = row * p.nsplit_grid + split;
-            if (p.local_merge) {
+            if (!PAGED && !Q8 && p.local_merge) {
                 st_pol4<0>(rpo, (uint32_t)((slot * D + 4 * d4) * 4), O);
                 if (d4 == 0) st_pol2<0>(rpml, (uint32_t)(slot * 8), float2{M, L});
             } else {
@@ -981,7 +981,7 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8, KPW) * 64, wgs_per_cu(PAGED, Q
         wait_vmem();
         __syncthreads();
         stamp(5);
-        if (p.local_merge) {
+        if (!PAGED && !Q8 && p.local_merge) {
             // XCD-local form (every workgroup of the group runs on one XCD; the launcher sets it
             // only for fixed mergers and grids whose groups map to one XCD each): the partials
             // are in this XCD's L2 (completed, above); the split's flag word, also a plain
@@ -1000,6 +1000,10 @@ __global__ __launch_bounds__(waves_for(PAGED, Q8, KPW) * 64, wgs_per_cu(PAGED, Q
                 const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
                 bool done = false;
                 while (true) {
+                    // drop this CU's L1 copies first, so the flags (and, after the last round,
+                    // the partials) are read from the XCD's L2, whatever the load policy's L1
+                    // behaviour; a vector-cache invalidate, completed before the loads
+                    asm volatile("buffer_inv sc0\n\ts_waitcnt vmcnt(0)" ::: "memory");
                     bool ready = true;
                     for (int j = lane; j < nsp; j += 64) ready = ready && ld_pol1<kCpolSc0>(rfl, (uint32_t)j * 4u) == target;
                     if (__builtin_amdgcn_ballot_w64(!ready) == 0) {
