@@ -120,6 +120,10 @@ int max_splits() {
 // Decode placement and merge form: the environment's choice, read once, until
 // friday_attn_set_decode_form overrides it for the process.
 std::atomic<int> g_local_merge{-1}, g_split_major{-1}, g_kv_pair{-1};
+int q8_deep_default() {
+    static const int v = env_int("FRIDAY_ATTN_Q8_DEEP", 0, 0, 1);
+    return v;
+}
 int kv_pair_for(bool paged, int Hkv, int ngb) {
     static const int v = env_int("FRIDAY_ATTN_KV_PAIR", 0, 0, 1);
     const int o = g_kv_pair.load(std::memory_order_relaxed);

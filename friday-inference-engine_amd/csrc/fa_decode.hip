@@ -340,10 +340,13 @@ constexpr int wgs_per_cu(bool paged, bool q8, int kpw = 1) { return kpw == 2 ? 1
 // walks kv-head pairs, waves [0, 4) take kv head 2x and waves [4, 8) kv head 2x + 1 over the
 // same positions, so a workgroup reads twice the bytes of each cache row (two adjacent
 // kv-head slices); the pair is the merge group.
-template <int D, bool PAGED, bool Q8, int NST, bool ROPE, int KPW>
-__global__ __launch_bounds__(waves_for(PAGED, Q8, KPW) * 64, wgs_per_cu(PAGED, Q8, KPW)) void fa_decode_kernel(DecodeParams p) {
+// WOV > 0 overrides the wave count (contiguous int8, one kv head: 4 waves with NST = 2, a
+// second tile in flight while a wave dequantises; one workgroup per CU).
+template <int D, bool PAGED, bool Q8, int NST, bool ROPE, int KPW, int WOV = 0>
+__global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ? 1 : wgs_per_cu(PAGED, Q8, KPW)) void fa_decode_kernel(DecodeParams p) {
     static_assert(KPW == 1 || (KPW == 2 && !PAGED), "kv-head pairs: contiguous caches");
-    constexpr int W = waves_for(PAGED, Q8, KPW);  // waves of this workgroup
+    static_assert(WOV == 0 || (Q8 && !PAGED && KPW == 1), "wave override: contiguous int8");
+    constexpr int W = WOV ? WOV : waves_for(PAGED, Q8, KPW);  // waves of this workgroup
     constexpr int WT = W / KPW;                    // waves per kv head (tile interleave)
     constexpr int NT = W * 64;
     using Gm = Geo<D, Q8, PAGED, W>;
@@ -1092,14 +1095,14 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
     merge_any<D, kThreads>(p, (size_t)row, 1, nsp);
 }
 
-template <int D, bool PAGED, bool Q8, int KPW>
+template <int D, bool PAGED, bool Q8, int KPW, int WOV = 0, int NSTQ = kStagesQ8>
 int launch_k(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
     p.split_major = split_major_default();
     const dim3 grid(p.Hkv / KPW * p.ngb, p.single ? 1 : p.nsplit_grid, batch);
-    const dim3 block(waves_for(PAGED, Q8, KPW) * 64);
+    const dim3 block((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64);
     // fixed mergers while the whole grid can be resident at once, else the last arriver merges
-    const size_t resident = (size_t)device_cus() * wgs_per_cu(PAGED, Q8, KPW);
+    const size_t resident = (size_t)device_cus() * (WOV ? 1 : wgs_per_cu(PAGED, Q8, KPW));
     p.merge_slices = (size_t)grid.x * grid.y * grid.z <= resident ? kMergeSlices : 0;
     // XCD-local merge: fixed mergers, contiguous fp16 caches, groups placed one XCD each
     // (workgroup ids are dealt to the 8 XCDs in turn, and a group's ids are congruent modulo
@@ -1110,11 +1113,11 @@ int launch_k(const DecodeParams& p_in, int batch, hipStream_t stream) {
                         : 0;
     if (p.rope_table) {
         if (!p.counters || (PAGED && Q8)) return -2;  // the step needs the fused merge; no int8 pages
-        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, true, KPW>), grid, block, 0,
+        hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? NSTQ : kStages, true, KPW, WOV>), grid, block, 0,
                            stream, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? kStagesQ8 : kStages, false, KPW>), grid, block, 0, stream,
+    hipLaunchKernelGGL((fa_decode_kernel<D, PAGED, Q8, Q8 ? NSTQ : kStages, false, KPW, WOV>), grid, block, 0, stream,
                        p);
     if (hipGetLastError() != hipSuccess) return -1;
     if (!p.single && !p.counters) {
@@ -1133,6 +1136,9 @@ int launch_t(const DecodeParams& p, int batch, hipStream_t stream) {
             if (p.ngb != 1 || p.Hkv % 2) return -2;
             return launch_k<D, PAGED, Q8, 2>(p, batch, stream);
         }
+        // contiguous int8, one kv head per workgroup: 4 waves, two tiles in flight each
+        // (FRIDAY_ATTN_Q8_DEEP = 1; the default is 8 waves with one)
+        if constexpr (Q8) if (q8_deep_default()) return launch_k<D, PAGED, Q8, 1, 4, 2>(p, batch, stream);
     }
     return launch_k<D, PAGED, Q8, 1>(p, batch, stream);
 }
