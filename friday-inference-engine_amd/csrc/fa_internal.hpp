@@ -138,6 +138,7 @@ struct PrefillParams {
     const int* d_pos0;
     int T, Hq, Hkv, G;
     float scale2;
+    int prefetch2;         // fp16 caches: copy the first two stages at the start (set by the launcher)
 };
 
 int launch_prefill(const PrefillParams& p, int head_dim, bool q8, hipStream_t stream);

@@ -419,18 +419,21 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             }
             __syncthreads();
         } else {
-            // the DMA of `tile` is the only one in flight: wait for it; after the barrier every
-            // wave's part of the stage has landed and every wave is done with the other stage
+            // the DMA of `tile` is the only one in flight (at tile 0 with prefetch2, tile 1's
+            // too): wait for it; after the barrier every wave's part of the stage has landed and
+            // every wave is done with the other stage
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             const unsigned char* sk = B ? stage1 : stage0;
             // the next stage's DMA into the other buffer, in flight during this stage's compute:
             // the K part of the next stage first, its V part once this stage's S^T MFMAs are
-            // issued (measured 1 % faster than both at once at config 4, p0 = 7680)
+            // issued (measured 1 % faster than both at once at config 4, p0 = 7680); with
+            // prefetch2, stage 1 went out with stage 0 at the start
             using SN = std::integral_constant<int, 1 - B>;
-            if (tile + 1 < ntiles) issue(tile + 1, SN{}, std::integral_constant<int, 1>{});
+            const bool next = tile + 1 < ntiles && !(tile == 0 && p.prefetch2);
+            if (next) issue(tile + 1, SN{}, std::integral_constant<int, 1>{});
             compute(n_tag, sk, sk + Gm::STAGE_K, kpos0, [&] {
-                if (tile + 1 < ntiles) issue(tile + 1, SN{}, std::integral_constant<int, 2>{});
+                if (next) issue(tile + 1, SN{}, std::integral_constant<int, 2>{});
             });
         }
     };
@@ -448,7 +451,12 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         if (ntiles > 1) issue_q8(1);
         __syncthreads();
     } else {
+        // both stage buffers are free at the start: with prefetch2 the copy of stage 1 goes
+        // out right behind stage 0's, so the first wait covers both and the copy of stage 2
+        // is the first to overlap a stage's compute (one copy latency less per launch; the
+        // waits stay full vmcnt(0) waits)
         issue(0, S0{}, std::integral_constant<int, 0>{});
+        if (p.prefetch2 && ntiles > 1) issue(1, S1{}, std::integral_constant<int, 0>{});
     }
     if (RA == RB || grp == 0) {
         for (int tile = 0; tile < ntiles; tile += 2) {
@@ -526,7 +534,14 @@ int launch_dma(const PrefillParams& p, hipStream_t stream) {
 // wave so that the registers of two waves per SIMD hold them (RT 1..6: (1,0), (1,1),
 // (2,1), (2,2), (3,2), (3,3)).
 template <int D, bool Q8, bool BF = false>
-int launch_dma_rt(const PrefillParams& p, hipStream_t stream) {
+int launch_dma_rt(const PrefillParams& p_in, hipStream_t stream) {
+    // FRIDAY_ATTN_PREFILL_PREFETCH2 = 0 turns the two-stage start off
+    static const int prefetch2 = [] {
+        const char* e = std::getenv("FRIDAY_ATTN_PREFILL_PREFETCH2");
+        return e && *e ? std::atoi(e) != 0 : 1;
+    }();
+    PrefillParams p = p_in;
+    p.prefetch2 = Q8 ? 0 : prefetch2;
     static const int forced = [] {
         const char* e = std::getenv("FRIDAY_ATTN_PREFILL_RT");
         return e && *e ? std::atoi(e) : 0;
