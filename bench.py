@@ -250,6 +250,12 @@ def cpu_baseline(S, Hq, Hkv, d, budget_s, threads=None):
                       f"{el:.1f} s; {what}; host logical CPUs {ncpu}"}
 
 
+def decode_form():
+    """The decode placement / merge switches this process runs with (environment)."""
+    return {k.lower().replace("friday_attn_", ""): os.environ.get(k, "0") for k in
+            ("FRIDAY_ATTN_LOCAL_MERGE", "FRIDAY_ATTN_SPLIT_MAJOR", "FRIDAY_ATTN_KV_PAIR", "FRIDAY_ATTN_Q8_DEEP")}
+
+
 def headline(cx, args):
     S, L, Hq, Hkv, d = args.ctx, args.layers, 40, 8, 128
     log(f"[bench] config 3: S={S} layers={L} {Hq}q/{Hkv}kv d{d}, {2 * L * S * Hkv * d * 2 / 2**30:.2f} GiB KV")
@@ -289,6 +295,7 @@ def headline(cx, args):
                    "layers": L, "ctx": S, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": d},
         "us_per_layer_step": round(us_layer, 3),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_form": decode_form(),
         "tokens_per_s": round(1e3 / ms_step, 2),
         "decode_only_launch_us": round(ms_dec * 1e3 / L, 3),
         "roofline": {"bound": "hbm", "kernel": "fa_decode_kernel (step variant: friday_attn_decode_step)",
@@ -627,7 +634,7 @@ def q8_config(cx, S, L, steps, warmup):
         b.free()
     us = ms * 1e3 / L
     nbytes = 2 * (lb + sb)
-    return {"config": "3 with int8 KV (--kv q8)", "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
+    return {"config": "3 with int8 KV (--kv q8)", "decode_form": decode_form(), "ctx": S, "layers": L, "heads": f"{Hq}q/{Hkv}kv d{d}",
             "us_per_layer_step": round(us, 3), "kv_bytes_per_layer": nbytes, "kv_GBps": round(nbytes / us / 1e3, 1),
             "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "tokens_per_s": round(1e6 / (us * L), 2)}
 
