@@ -163,12 +163,19 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
             qf[rt][s] = *reinterpret_cast<const h8*>(&raw);
         }
     }
-    // settle the q loads here: the compiler would otherwise wait for them at their first
-    // use inside the stage loop, in every iteration, behind the stage copies
+    // The q loads are settled once, right after the first stage copies are issued (below):
+    // the compiler would otherwise wait for them at their first use inside the stage loop, in
+    // every iteration, behind the stage copies; settling them here, before any copy is
+    // issued, would put a whole q round trip in front of the first copy.
+    auto settle_q = [&]() __attribute__((always_inline)) {
+        // a full wait: the copies issued after the q loads are invisible to the compiler's
+        // counting, so its partial waits would rely on the two kinds retiring in order
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int s = 0; s < Gm::KSTEPS; ++s) asm volatile("" ::"v"(qf[rt][s]));
+            for (int s = 0; s < Gm::KSTEPS; ++s) asm volatile("" ::"v"(qf[rt][s]));
+    };
     const int last_row = min(wg_row0 + (RA + RB) * 16, R) - 1;
     const int kend = p0 + last_row / p.G + 1;  // keys [0, kend) for the workgroup
     const int ntiles = (kend + kP2KS - 1) / kP2KS;
@@ -446,6 +453,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
     using NB = std::integral_constant<int, RB>;
     if constexpr (Q8) {
         issue_q8(0);
+        settle_q();  // q and stage 0's codes and scales were in flight together
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         decode_q8(stage0);
         if (ntiles > 1) issue_q8(1);
@@ -457,6 +465,7 @@ __global__ __launch_bounds__(kP2Threads) void fa_prefill_dma_kernel(PrefillParam
         // waits stay full vmcnt(0) waits)
         issue(0, S0{}, std::integral_constant<int, 0>{});
         if (p.prefetch2 && ntiles > 1) issue(1, S1{}, std::integral_constant<int, 0>{});
+        settle_q();  // q and the first copies were in flight together
     }
     if (RA == RB || grp == 0) {
         for (int tile = 0; tile < ntiles; tile += 2) {
