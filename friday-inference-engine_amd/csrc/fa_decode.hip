@@ -398,16 +398,20 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
     const int nsp = p.single ? 1 : split_count(S, p.min_chunk, p.max_splits);
     if (split >= nsp) return;  // inactive split; the merge ignores it
     // fused merge (see the end of the kernel): in the fixed-merger form, this workgroup's
-    // merge slice (mk >= 0 for the last nslice splits); the group's counter base, loaded
-    // early by the workgroups that need it (mergers, or every one in the last-arriver form)
+    // merge slice (mk >= 0 for the last nslice splits)
     const bool last_arriver = p.merge_slices == 0;
     const int nslice = (nsp > 1 && p.counters && !last_arriver) ? merge_slices<D>(p, nsp) : 1;
     const int mk = split - (nsp - nslice);
     // (grid x = Hkv * ngb groups)
     unsigned* cnt = reinterpret_cast<unsigned*>(p.counters) + ((size_t)b * ngroups + group) * kCounterStride;
+    // The group's counter base is loaded by the workgroups that need it (mergers; every one
+    // in the last-arriver and XCD-local forms) right after their first tile loads (in
+    // stream, below). Loaded here, before them, its round trip to the memory side came
+    // before the first tile: the compiler placed a full wait for it ahead of the first loads
+    // (it reused the load's destination register as the unused high half of an address
+    // computation). After the stream, the compiler waited for it before the combine.
+    const bool needs_base = nsp > 1 && p.counters && (mk >= 0 || last_arriver || p.local_merge);
     unsigned base = 0;
-    if (nsp > 1 && p.counters && (mk >= 0 || last_arriver || p.local_merge))
-        base = __hip_atomic_load(cnt + kCounterStride / 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int start = split * chunk;
     const int end = min(S, start + chunk);  // positions [start, end)
 #if FA_STAMPS
@@ -441,13 +445,14 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
     constexpr int CW = Q8 ? 16 : 8;                       // values of one row chunk
     constexpr int NH = ROPE ? CW / 8 : 1;                 // fp16 vectors of one row chunk
     // q rotation. Contiguous caches: every lane rotates its own fragment in registers (no LDS,
-    // no barrier) with the RoPE table entries of its own pairs, qcs (NeoX: i = 32 s + 8 kb + j,
-    // s < KSTEPS/2, partner in k-step s + KSTEPS/2 of the same lane; interleaved:
-    // i = 16 s + 4 kb + j, pair (2j, 2j + 1) of k-step s). Paged (a smaller register budget):
-    // the rotation is spread over the workgroup (rq0, rq1, rcs) and read back through LDS.
+    // no barrier). Lane i holds RoPE table entry i of the position (crow, one 8-byte load), and
+    // a lane takes the entries of its own pairs from the lanes holding them (ds_bpermute:
+    // NeoX pair i = 32 s + 8 kb + j, s < KSTEPS/2, partner in k-step s + KSTEPS/2 of the same
+    // lane; interleaved: i = 16 s + 4 kb + j, pair (2j, 2j + 1) of k-step s). Paged (a smaller
+    // register budget): the rotation is spread over the workgroup (rq0, rq1, rcs) and read
+    // back through LDS.
     constexpr bool QREG = ROPE && !PAGED;
-    constexpr int NQC = QREG ? D / 8 : 1;
-    float2 qcs[NQC];
+    float2 crow = float2{0.f, 0.f};
     _Float16 rq0[PPT], rq1[PPT];
     float2 rcs[PPT];
     h8 nk[NH], nkp[NH], nv[NH];
@@ -480,30 +485,15 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
             qf[s] = *reinterpret_cast<const h8*>(&raw);
         }
         if constexpr (!ROPE) return;
+        // Every load below is issued by every wave, whatever rot_q, the pair layout or the
+        // wave's role (loads it does not need go through a descriptor of size 0: zeros, no
+        // memory access). The compiler counts outstanding loads along each path; where paths
+        // with different load counts join it keeps the smallest count, and the waits of the
+        // q rotation then drained the first K/V tiles issued after these loads as well.
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
-        if constexpr (QREG) if (rot_q) {
-            if (p.neox) {
-#pragma unroll
-                for (int s = 0; s < Gm::KSTEPS / 2; ++s)
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        const f4 c2 = *reinterpret_cast<const f4*>(cs + 32 * s + 8 * kb + j);
-                        qcs[8 * s + j] = float2{c2[0], c2[1]};
-                        qcs[8 * s + j + 1] = float2{c2[2], c2[3]};
-                    }
-            } else {
-#pragma unroll
-                for (int s = 0; s < Gm::KSTEPS; ++s)
-#pragma unroll
-                    for (int j = 0; j < 4; j += 2) {
-                        const f4 c2 = *reinterpret_cast<const f4*>(cs + 16 * s + 4 * kb + j);
-                        qcs[4 * s + j] = float2{c2[0], c2[1]};
-                        qcs[4 * s + j + 1] = float2{c2[2], c2[3]};
-                    }
-            }
-        }
-        if constexpr (!QREG) if (rot_q) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
+        if constexpr (QREG) crow = cs[lane < HD2 ? lane : HD2 - 1];
+        if constexpr (!QREG) {  // this thread's share of the q rotation: PPT pairs of head column tid / TPH
             const int hg = gb * 16 + tid / TPH, i0 = (tid % TPH) * PPT;
             const uint16_t* qr = p.q + ((size_t)b * p.Hq + kvh * p.G + (hg < p.G ? hg : 0)) * D;
 #pragma unroll
@@ -514,7 +504,9 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
                 rcs[e] = cs[i];
             }
         }
-        // only the append wave needs the new row chunk (and its rotation partner) of its lane
+        // only the append wave needs the new row chunk (and its rotation partner) of its
+        // lane (its loads may sink behind the first tiles: that only makes this one wave's
+        // waits cover its own tiles)
         if (wt == append_wt) {
             const size_t src = (size_t)b * p.kv_dim + (size_t)kvh * D;
             const int partner = nchunk < HD2 ? nchunk + HD2 : nchunk - HD2;
@@ -539,90 +531,128 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
     u4 rk = u4{0, 0, 0, 0}, kq = u4{0, 0, 0, 0}, vq = u4{0, 0, 0, 0};
     float ksc = 0.0f, vsc = 0.0f;
     auto prepare = [&]() __attribute__((always_inline)) {
+        // Every value load_inputs fetched is used here whatever rot_q and the wave's role
+        // (results are then chosen by selects, and only the stores are conditional): a load
+        // whose value is used in one conditional block only is moved into that block by the
+        // compiler, behind the first K/V tiles, and its wait then drains those tiles too.
         if constexpr (ROPE) {
-            if constexpr (QREG) if (rot_q) {
+            if constexpr (QREG) {
+                // in place; each pair keeps its inputs when rot_q is false. The table entries
+                // of a k-step's 8 pairs are fetched from their lanes first (16 ds_bpermutes in
+                // flight), then the 8 pairs are rotated.
                 if (p.neox) {
                     constexpr int KH = Gm::KSTEPS / 2;
 #pragma unroll
-                    for (int s = 0; s < KH; ++s)
+                    for (int s = 0; s < KH; ++s) {
+                        float c[8], sn[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int i = 32 * s + 8 * kb + j;
+                            c[j] = __shfl(crow.x, i, 64);
+                            sn[j] = __shfl(crow.y, i, 64);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);  // keep the 16 fetches together
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
                             _Float16 r0, r1;
-                            rope_rotate((float)qf[s][j], (float)qf[s + KH][j], qcs[8 * s + j].x, qcs[8 * s + j].y, r0, r1);
-                            qf[s][j] = r0;
-                            qf[s + KH][j] = r1;
+                            const _Float16 x0 = qf[s][j], x1 = qf[s + KH][j];
+                            rope_rotate((float)x0, (float)x1, c[j], sn[j], r0, r1);
+                            qf[s][j] = rot_q ? r0 : x0;
+                            qf[s + KH][j] = rot_q ? r1 : x1;
                         }
+                    }
                 } else {
 #pragma unroll
-                    for (int s = 0; s < Gm::KSTEPS; ++s)
+                    for (int s = 0; s < Gm::KSTEPS; s += 2) {
+                        float c[8], sn[8];
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            _Float16 r0, r1;
-                            rope_rotate((float)qf[s][2 * j], (float)qf[s][2 * j + 1], qcs[4 * s + j].x, qcs[4 * s + j].y, r0, r1);
-                            qf[s][2 * j] = r0;
-                            qf[s][2 * j + 1] = r1;
+                        for (int t = 0; t < 8; ++t) {
+                            const int i = 16 * (s + t / 4) + 4 * kb + (t % 4);
+                            c[t] = __shfl(crow.x, i, 64);
+                            sn[t] = __shfl(crow.y, i, 64);
                         }
+                        __builtin_amdgcn_sched_barrier(0);  // keep the 16 fetches together
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            const int ss = s + t / 4, j = t % 4;
+                            _Float16 r0, r1;
+                            const _Float16 x0 = qf[ss][2 * j], x1 = qf[ss][2 * j + 1];
+                            rope_rotate((float)x0, (float)x1, c[t], sn[t], r0, r1);
+                            qf[ss][2 * j] = rot_q ? r0 : x0;
+                            qf[ss][2 * j + 1] = rot_q ? r1 : x1;
+                        }
+                    }
                 }
             }
-            if constexpr (!QREG) if (rot_q) {
+            if constexpr (!QREG) {
                 // The rotation of the group's q rows is spread over the workgroup (thread t:
                 // rotation pairs i0 .. i0 + PPT - 1 of head column t / TPH, from the values
-                // load_inputs fetched), and every lane reads its rotated fragment back from LDS.
+                // load_inputs fetched; unrotated when rot_q is false), and every lane reads
+                // its fragment back from LDS.
                 _Float16* qx = reinterpret_cast<_Float16*>(smem + Gm::QX_OFF);  // [16 heads][D]
                 const int hc = tid / TPH, i0 = (tid % TPH) * PPT;
 #pragma unroll
                 for (int e = 0; e < PPT; ++e) {
-                    if (p.neox)
-                        rope_rotate((float)rq0[e], (float)rq1[e], rcs[e].x, rcs[e].y, qx[hc * D + i0 + e],
-                                    qx[hc * D + HD2 + i0 + e]);
-                    else
-                        rope_rotate((float)rq0[e], (float)rq1[e], rcs[e].x, rcs[e].y, qx[hc * D + 2 * (i0 + e)],
-                                    qx[hc * D + 2 * (i0 + e) + 1]);
+                    _Float16 r0, r1;
+                    rope_rotate((float)rq0[e], (float)rq1[e], rcs[e].x, rcs[e].y, r0, r1);
+                    r0 = rot_q ? r0 : rq0[e];
+                    r1 = rot_q ? r1 : rq1[e];
+                    if (p.neox) {
+                        qx[hc * D + i0 + e] = r0;
+                        qx[hc * D + HD2 + i0 + e] = r1;
+                    } else {
+                        qx[hc * D + 2 * (i0 + e)] = r0;
+                        qx[hc * D + 2 * (i0 + e) + 1] = r1;
+                    }
                 }
                 __syncthreads();
 #pragma unroll
                 for (int s = 0; s < Gm::KSTEPS; ++s) qf[s] = *reinterpret_cast<const h8*>(qx + col * D + s * 32 + kb * 8);
             }
             if (wt == append_wt) {
-                h8 r[NH];
+            h8 r[NH];
 #pragma unroll
-                for (int i = 0; i < NH; ++i) {
-                    const h8 x = nk[i], y = nkp[i];
-                    if (p.neox) {
-                        const bool lo = nchunk < HD2;
+            for (int i = 0; i < NH; ++i) {
+                const h8 x = nk[i], y = nkp[i];
+                if (p.neox) {
+                    const bool lo = nchunk < HD2;
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            _Float16 r0, r1;
-                            const float2 c = ncs[8 * i + j];
-                            // pair (i, i + D/2): x0 is the low-half element
-                            rope_rotate((float)(lo ? x[j] : y[j]), (float)(lo ? y[j] : x[j]), c.x, c.y, r0, r1);
-                            r[i][j] = lo ? r0 : r1;
-                        }
-                    } else {
+                    for (int j = 0; j < 8; ++j) {
+                        _Float16 r0, r1;
+                        const float2 c = ncs[8 * i + j];
+                        // pair (i, i + D/2): x0 is the low-half element
+                        rope_rotate((float)(lo ? x[j] : y[j]), (float)(lo ? y[j] : x[j]), c.x, c.y, r0, r1);
+                        r[i][j] = lo ? r0 : r1;
+                    }
+                } else {
 #pragma unroll
-                        for (int j = 0; j < 8; j += 2) {
-                            _Float16 r0, r1;
-                            const float2 c = ncs[8 * i + j];
-                            rope_rotate((float)x[j], (float)x[j + 1], c.x, c.y, r0, r1);
-                            r[i][j] = r0;
-                            r[i][j + 1] = r1;
-                        }
+                    for (int j = 0; j < 8; j += 2) {
+                        _Float16 r0, r1;
+                        const float2 c = ncs[8 * i + j];
+                        rope_rotate((float)x[j], (float)x[j + 1], c.x, c.y, r0, r1);
+                        r[i][j] = r0;
+                        r[i][j + 1] = r1;
                     }
                 }
+            }
+            uint16_t kbits = 0, vbits = 0;
+            if constexpr (!Q8) {
+                rk = *reinterpret_cast<const u4*>(&r[0]);
+            } else {
+                // int8 cache: the rotated k (rounded to fp16 as the rope step leaves it) and
+                // v are quantized per 32-value block (this lane's 16 values and those of
+                // lane ^ 1) exactly as the int8 append does (storeKvQ8Kernel rules)
+                quant_chunk16(r, kq, ksc, kbits);
+                quant_chunk16(nv, vq, vsc, vbits);
+            }
+            {
                 const size_t dst = row_index<PAGED>(p, b, S - 1) * p.kv_dim + (size_t)kvh * D + nchunk;
                 if constexpr (!Q8) {
-                    rk = *reinterpret_cast<const u4*>(&r[0]);
                     if (lane < Gm::CPR) {
                         *reinterpret_cast<u4*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.k)) + dst) = rk;
                         *reinterpret_cast<h8*>(const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(p.v)) + dst) = nv[0];
                     }
                 } else {
-                    // int8 cache: the rotated k (rounded to fp16 as the rope step leaves it) and
-                    // v are quantized per 32-value block (this lane's 16 values and those of
-                    // lane ^ 1) exactly as the int8 append does (storeKvQ8Kernel rules)
-                    uint16_t kbits, vbits;
-                    quant_chunk16(r, kq, ksc, kbits);
-                    quant_chunk16(nv, vq, vsc, vbits);
                     if (lane < Gm::CPR) {
                         *reinterpret_cast<u4*>(const_cast<char*>(static_cast<const char*>(p.k)) + dst) = kq;
                         *reinterpret_cast<u4*>(const_cast<char*>(static_cast<const char*>(p.v)) + dst) = vq;
@@ -632,6 +662,7 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
                         }
                     }
                 }
+            }
             }
         }
         if (!gvalid) {
@@ -844,9 +875,15 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
         Stage st[N];
         const int groups = (my_tiles + N - 1) / N;
         if (ROPE) load_inputs();
-        if (groups > 0) {
+        // unconditional, like the loads above (a wave without tiles reads nothing: its
+        // tiles lie past the split's end)
 #pragma unroll
-            for (int s = 0; s < N; ++s) load_tile(st[s], wt + s * WT);
+        for (int s = 0; s < N; ++s) load_tile(st[s], wt + s * WT);
+        {
+            // agent-coherent (sc1) like the relaxed agent-scope atomic load it replaces;
+            // size 0 (a zero, no access) for the workgroups that do not merge
+            const __amdgpu_buffer_rsrc_t rb = coherent_rsrc(cnt + kCounterStride / 2, needs_base ? 4u : 0u);
+            base = (unsigned)__builtin_amdgcn_raw_buffer_load_b32(rb, 0, 0, kCpolSc1);
         }
         if (!ROPE) load_inputs();
         using Whole = std::integral_constant<int, 0>;
