@@ -879,13 +879,14 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
         // tiles lie past the split's end)
 #pragma unroll
         for (int s = 0; s < N; ++s) load_tile(st[s], wt + s * WT);
+        if (!ROPE) load_inputs();
         {
-            // agent-coherent (sc1) like the relaxed agent-scope atomic load it replaces;
-            // size 0 (a zero, no access) for the workgroups that do not merge
+            // the newest load, so that no wait for the others covers it. Agent-coherent (sc1)
+            // like the relaxed agent-scope atomic load it replaces; size 0 (a zero, no
+            // access) for the workgroups that do not merge
             const __amdgpu_buffer_rsrc_t rb = coherent_rsrc(cnt + kCounterStride / 2, needs_base ? 4u : 0u);
             base = (unsigned)__builtin_amdgcn_raw_buffer_load_b32(rb, 0, 0, kCpolSc1);
         }
-        if (!ROPE) load_inputs();
         using Whole = std::integral_constant<int, 0>;
         if constexpr (ROPE && !Q8 && N > 1) {
             // Short splits (all of a wave's tiles in flight at once): the first tile goes into
