@@ -47,22 +47,36 @@ __global__ __launch_bounds__(256) void fa_rope_store_kernel(RopeParams p) {
     const int pos = PAGED ? p.seq_lens[t] - 1 : (p.d_pos ? *p.d_pos : p.pos) + t;
     if (pos < 0 || pos >= p.max_ctx) return;
     const float2* cs = reinterpret_cast<const float2*>(p.table) + (size_t)pos * hd2;
+    // every table entry of this thread is loaded before any q / k value is touched: with the
+    // loads inside the rotation loop the compiler converted the first chunk (waiting for it)
+    // before issuing them, so their round trip followed the chunk's instead of overlapping it
+    // (NeoX: the 8 entries of elements e0 .. e0 + 7; interleaved: the 4 entries e0/2 ..
+    // e0/2 + 3 of its 4 pairs, in ct[0..3], the last two loads repeating the first two)
+    float2 ct[8];
+    const int c0 = p.neox ? e0 : (e0 >> 1);
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        const f4 c2 = *reinterpret_cast<const f4*>(cs + c0 + (p.neox ? j : (j & 2)));
+        ct[j] = float2{c2[0], c2[1]};
+        ct[j + 1] = float2{c2[2], c2[3]};
+    }
+    // the chunk values are first needed here, after the table loads went out (the memory
+    // clobber keeps those loads above this point; the chunk registers stay untouched until it)
+    asm volatile("" ::"v"(a), "v"(bv) : "memory");
     h8 ra, rb;
     if (p.neox) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float2 r = cs[e0 + j];
             _Float16 r0, r1;
-            rope_rotate((float)a[j], (float)bv[j], r.x, r.y, r0, r1);
+            rope_rotate((float)a[j], (float)bv[j], ct[j].x, ct[j].y, r0, r1);
             ra[j] = r0;
             rb[j] = r1;
         }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-            const float2 r = cs[(e0 + j) >> 1];
             _Float16 r0, r1;
-            rope_rotate((float)a[j], (float)a[j + 1], r.x, r.y, r0, r1);
+            rope_rotate((float)a[j], (float)a[j + 1], ct[j >> 1].x, ct[j >> 1].y, r0, r1);
             ra[j] = r0;
             ra[j + 1] = r1;
         }
