@@ -317,6 +317,40 @@ __device__ __forceinline__ uint16_t epilogue(float acc, const float* bias, const
     return h;
 }
 
+// The same with the bias and residual values loaded beforehand (present: hb / hr).
+__device__ __forceinline__ uint16_t epilogue_pre(float acc, bool hb, float b, bool hr, uint16_t r) {
+    uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)acc);
+    if (hb) {
+        float t = half_bits(h);
+        if (__builtin_isnan(t)) t = 0.0f;
+        if (__builtin_isnan(b)) b = 0.0f;
+        h = clamp_to_half_bits(t + b);
+    }
+    if (hr) {
+        float t = half_bits(r), a = half_bits(h);
+        if (__builtin_isnan(t)) t = 0.0f;
+        if (__builtin_isnan(a)) a = 0.0f;
+        h = clamp_to_half_bits(t + a);
+    }
+    return h;
+}
+
+// A decode-GEMV wave's epilogue operands, loaded when the wave starts (after its reduction
+// they cost two more dependent round trips): bias[row] and res[row] through descriptors of
+// size 0 when absent (zeros, no access; rows past N read zeros too).
+struct GemvEpi {
+    float b;
+    uint16_t r;
+};
+__device__ __forceinline__ GemvEpi gemv_epi_load(const KqGemvParams& p, int row) {
+    const __amdgpu_buffer_rsrc_t rb = uniform_rsrc(p.bias, p.bias ? (uint32_t)p.N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rr = uniform_rsrc(p.res, p.res ? (uint32_t)p.N * 2u : 0u);
+    GemvEpi e;
+    e.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, row * 4, 0, 0));
+    e.r = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rr, row * 2, 0, 0);
+    return e;
+}
+
 // Workgroup shape: WVN x WVT waves, each owning TN x TT tiles of 32 x 32 (rows x tokens),
 // so BN = 32 WVN TN weight rows and BT = 32 WVT TT tokens per workgroup. Staging: thread
 // u < 2 BN decodes half u % 2 (32 values) of weight row u / 2 of each stage, thread
@@ -581,6 +615,7 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
         row -= p.N;
     }
     const uint8_t* wrow = W + (size_t)row * p.row_bytes;
+    const GemvEpi epi = gemv_epi_load(p, row);
     const int nblk = p.K / 32;
     float acc = 0.0f;
     for (int blk = lane; blk < nblk; blk += 64) {
@@ -606,7 +641,7 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
+    if (lane == 0) y[row] = epilogue_pre(acc, p.bias != nullptr, epi.b, p.res != nullptr, epi.r);
 }
 
 // LDS-staged decode GEMV: a workgroup of ROWS waves takes ROWS consecutive weight rows
@@ -696,6 +731,7 @@ __global__ __launch_bounds__(64 * ROWS * WPR) void kq_gemv_lds_kernel(KqGemvPara
     const uint8_t* src = W + (size_t)n0 * p.row_bytes;  // 4-byte aligned: W is, n0 is even, row_bytes even
     gv_lds_u8* lds = (gv_lds_u8*)rows_lds;
     constexpr int NW = ROWS * WPR;  // waves; wave w takes row w % ROWS, block slice w / ROWS
+    const GemvEpi epi = gemv_epi_load(p, n0 + wave % ROWS);  // (rows past the group: unused)
     copy_span(src, span, lds, wave, NW, lane);
     // XL: the activations (xq: K bytes, 16-byte aligned; xd: K / 8 bytes) after the rows, at
     // xoff = ROWS row_bytes rounded up to 256
@@ -725,7 +761,7 @@ __global__ __launch_bounds__(64 * ROWS * WPR) void kq_gemv_lds_kernel(KqGemvPara
     }
     if (rw >= nrows) return;
     const int row = n0 + rw;
-    if (lane == 0) y[row] = epilogue(acc, p.bias, p.res, row);
+    if (lane == 0) y[row] = epilogue_pre(acc, p.bias != nullptr, epi.b, p.res != nullptr, epi.r);
 }
 
 // quantize_x_q8_kernel semantics (hpc_k_quants.cu:386-400): 32 lanes per 32-value block,
