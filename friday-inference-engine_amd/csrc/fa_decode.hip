@@ -362,7 +362,9 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
     pin_sgpr(p.q); pin_sgpr(p.k); pin_sgpr(p.v); pin_sgpr(p.d_pos); pin_sgpr(p.seq_len); pin_sgpr(p.max_seq);
     pin_sgpr(p.Hq); pin_sgpr(p.G); pin_sgpr(p.ngb); pin_sgpr(p.kv_dim); pin_sgpr(p.single);
     pin_sgpr(p.min_chunk); pin_sgpr(p.max_splits); pin_sgpr(p.counters); pin_sgpr(p.merge_slices);
-    pin_sgpr(p.Hkv); pin_sgpr(p.out_q); pin_sgpr(p.scale2); pin_sgpr(p.nsplit_grid);
+    pin_sgpr(p.Hkv); pin_sgpr(p.out_q); pin_sgpr(p.scale2); pin_sgpr(p.nsplit_grid); pin_sgpr(p.local_merge);
+    if (!PAGED) { pin_sgpr(p.split_major); pin_sgpr(p.flags); }
+    if (Q8) { pin_sgpr(p.k_scale); pin_sgpr(p.v_scale); }
     if (PAGED) { pin_sgpr(p.seq_lens); pin_sgpr(p.block_table); pin_sgpr(p.bt_stride); }
     if (ROPE) { pin_sgpr(p.rope_table); pin_sgpr(p.neox); pin_sgpr(p.k_new); pin_sgpr(p.v_new); }
     // int8 caches: the block scales of one position, for all kv heads, share a cache line, so
