@@ -70,6 +70,8 @@ class Ctx:
         self.bk.fabk_fill_normal_f16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
         self.bk.fabk_fill_normal_bf16.argtypes = [C.c_void_p, C.c_size_t, C.c_uint32, C.c_float, C.c_void_p]
         self.stream = fa.Stream()
+        if os.environ.get("FRIDAY_ATTN_LOCAL_MERGE") == "1":  # run the placement check before any capture
+            fa.setDecodeForm(1, -1, -1)
 
     def fill(self, buf, n_half, seed, scale=1.0, bf16=False):
         f = self.bk.fabk_fill_normal_bf16 if bf16 else self.bk.fabk_fill_normal_f16

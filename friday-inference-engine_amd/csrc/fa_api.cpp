@@ -317,6 +317,9 @@ int friday_attn_set_decode_form(int local_merge, int split_major, int kv_pair) {
     fa::g_local_merge.store(local_merge, std::memory_order_relaxed);
     fa::g_split_major.store(split_major, std::memory_order_relaxed);
     fa::g_kv_pair.store(kv_pair, std::memory_order_relaxed);
+    // the local form's placement check runs now (the null stream, synchronised), so that
+    // launches recorded into graphs later can use the form
+    if (local_merge == 1) fa::local_placement_ok(nullptr);
     return ok();
 }
 

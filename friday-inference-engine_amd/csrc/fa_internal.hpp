@@ -51,7 +51,9 @@ int device_cus();  // compute units of the current device
 int split_major_default();  // FRIDAY_ATTN_SPLIT_MAJOR (0 or 1), read once
 int local_merge_default();  // FRIDAY_ATTN_LOCAL_MERGE (0 or 1), read once
 int kv_pair_for(bool paged, int Hkv, int ngb);
-int q8_deep_default();  // FRIDAY_ATTN_Q8_DEEP (0 or 1), read once  // kv heads per decode workgroup (FRIDAY_ATTN_KV_PAIR)
+int q8_deep_default();  // FRIDAY_ATTN_Q8_DEEP (0 or 1), read once
+// XCD-local merge placement check of the current device (once; not while `stream` captures)
+bool local_placement_ok(hipStream_t stream);  // kv heads per decode workgroup (FRIDAY_ATTN_KV_PAIR)
 
 struct DecodeParams {
     const uint16_t* q;         // [B][Hq*D]

@@ -137,7 +137,10 @@ int friday_attn_decode_workspace_status(const void* workspace, size_t workspace_
  * other forms within the decode tolerance, not bit for bit. -1 restores the environment's
  * choice (FRIDAY_ATTN_LOCAL_MERGE, FRIDAY_ATTN_SPLIT_MAJOR, FRIDAY_ATTN_KV_PAIR; default 0).
  * Paged launches keep one kv head per workgroup and the counter merge. A captured launch
- * keeps the form it was recorded with. */
+ * keeps the form it was recorded with. The local form needs a one-time placement check per
+ * device (a few small launches and a synchronisation; no allocation): local_merge = 1 runs
+ * it here on the null stream; otherwise the first launch that wants the form and is not
+ * being captured runs it on its own stream, and until then launches use the counter form. */
 int friday_attn_set_decode_form(int local_merge, int split_major, int kv_pair);
 /* launchDecodeAttentionSplit in one kernel: the split partials are merged by the last
  * few workgroups of each kv head (the ones dispatched last), each over a slice of the
