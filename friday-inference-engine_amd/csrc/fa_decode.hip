@@ -1137,43 +1137,6 @@ __global__ __launch_bounds__(kThreads) void fa_merge_kernel(DecodeParams p) {
     merge_any<D, kThreads>(p, (size_t)row, 1, nsp);
 }
 
-// Placement check of the XCD-local merge: every workgroup of a (groups x splits) grid
-// records the XCD it runs on (HW_REG_XCC_ID) in a file-scope array (no allocation).
-constexpr int kProbeX = 64, kProbeY = 32;
-__device__ unsigned g_xcc_probe[kProbeX * kProbeY];
-__global__ void fa_xcc_probe_kernel(unsigned* xcc) {
-    if (threadIdx.x == 0) xcc[blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_getreg((3 << 11) | 20);
-}
-
-// Whether the workgroups of each group (grid x, a multiple of 8 columns) of a decode-shaped
-// grid run on one XCD on the current device: probed once per device (a 64 x 32 grid, 16
-// launches on the caller's stream, which is synchronised) and remembered. Not probed while
-// `stream` is capturing: the caller then uses the counter form.
-bool local_placement_ok(hipStream_t stream) {
-    static std::mutex mu;
-    static int state[64] = {};  // 0 unknown, 1 ok, -1 not
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    std::lock_guard<std::mutex> lock(mu);
-    if (state[dev]) return state[dev] > 0;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
-    void* d = nullptr;
-    bool ok = hipGetSymbolAddress(&d, HIP_SYMBOL(g_xcc_probe)) == hipSuccess;
-    std::vector<unsigned> h(kProbeX * kProbeY);
-    for (int r = 0; ok && r < 16; ++r) {
-        hipLaunchKernelGGL(fa_xcc_probe_kernel, dim3(kProbeX, kProbeY), dim3(64), 0, stream, static_cast<unsigned*>(d));
-        ok = hipGetLastError() == hipSuccess &&
-             hipMemcpyAsync(h.data(), d, sizeof(unsigned) * h.size(), hipMemcpyDeviceToHost, stream) == hipSuccess &&
-             hipStreamSynchronize(stream) == hipSuccess;
-        // workgroup ids are x + 64 y: every column x on one XCD for all y
-        for (int x = 0; ok && x < kProbeX; ++x)
-            for (int y = 1; ok && y < kProbeY; ++y) ok = h[x + kProbeX * y] == h[x];
-    }
-    state[dev] = ok ? 1 : -1;
-    return ok;
-}
-
 template <int D, bool PAGED, bool Q8, int KPW, int WOV = 0, int NSTQ = kStagesQ8>
 int launch_k(const DecodeParams& p_in, int batch, hipStream_t stream) {
     DecodeParams p = p_in;
@@ -1226,7 +1189,44 @@ __global__ void fa_zero_kernel(uint32_t* p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
 }
 
+// Placement check of the XCD-local merge: every workgroup of a (groups x splits) grid
+// records the XCD it runs on (HW_REG_XCC_ID) in a file-scope array (no allocation).
+constexpr int kProbeX = 64, kProbeY = 32;
+__device__ unsigned g_xcc_probe[kProbeX * kProbeY];
+__global__ void fa_xcc_probe_kernel(unsigned* xcc) {
+    if (threadIdx.x == 0) xcc[blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_getreg((3 << 11) | 20);
+}
+
 }  // namespace
+
+// Whether the workgroups of each group (grid x, a multiple of 8 columns) of a decode-shaped
+// grid run on one XCD on the current device: probed once per device (a 64 x 32 grid, 16
+// launches on the caller's stream, which is synchronised) and remembered. Not probed while
+// `stream` is capturing: the caller then uses the counter form.
+bool local_placement_ok(hipStream_t stream) {
+    static std::mutex mu;
+    static int state[64] = {};  // 0 unknown, 1 ok, -1 not
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    std::lock_guard<std::mutex> lock(mu);
+    if (state[dev]) return state[dev] > 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+    void* d = nullptr;
+    bool ok = hipGetSymbolAddress(&d, HIP_SYMBOL(g_xcc_probe)) == hipSuccess;
+    std::vector<unsigned> h(kProbeX * kProbeY);
+    for (int r = 0; ok && r < 16; ++r) {
+        hipLaunchKernelGGL(fa_xcc_probe_kernel, dim3(kProbeX, kProbeY), dim3(64), 0, stream, static_cast<unsigned*>(d));
+        ok = hipGetLastError() == hipSuccess &&
+             hipMemcpyAsync(h.data(), d, sizeof(unsigned) * h.size(), hipMemcpyDeviceToHost, stream) == hipSuccess &&
+             hipStreamSynchronize(stream) == hipSuccess;
+        // workgroup ids are x + 64 y: every column x on one XCD for all y
+        for (int x = 0; ok && x < kProbeX; ++x)
+            for (int y = 1; ok && y < kProbeY; ++y) ok = h[x + kProbeX * y] == h[x];
+    }
+    state[dev] = ok ? 1 : -1;
+    return ok;
+}
 
 int launch_zero_fill(void* ptr, size_t bytes, hipStream_t stream) {
     const size_t n = bytes / 4;
