@@ -111,16 +111,19 @@ __global__ __launch_bounds__(256) void fa_store_kv_q8_kernel(Q8StoreParams p) {
     const int blk = blockIdx.x * 8 + (threadIdx.x >> 5);
     const int nblk = p.kv_dim / 32;
     const int t = blockIdx.y;
-    const int pos = (p.d_pos ? *p.d_pos : p.pos) + t;
-    const bool active = blk < 2 * nblk && pos >= 0 && pos < p.max_ctx;
     const bool is_v = blk >= nblk;
     const int bb = is_v ? blk - nblk : blk;
-    float x = 0.0f;
-    if (active) {
-        const uint16_t* src = (is_v ? p.v : p.k) + (size_t)t * p.kv_dim;
-        x = (float)reinterpret_cast<const _Float16*>(src)[bb * 32 + lane];
-        if (__builtin_isnan(x)) x = 0.0f;
-    }
+    // the value is loaded before the position is read (its address does not depend on it),
+    // so the two round trips overlap
+    asm volatile("" ::"s"(p.k), "s"(p.v), "s"(p.d_pos), "s"(p.pos));  // one batch of argument loads
+    // straight-line: lanes past the last block read block 0 of k (a valid address; unused)
+    const bool in_row = blk < 2 * nblk;
+    const uint16_t* src = (in_row && is_v ? p.v : p.k) + (size_t)t * p.kv_dim;
+    const _Float16 xh = reinterpret_cast<const _Float16*>(src)[(in_row ? bb : 0) * 32 + lane];
+    const int pos = (p.d_pos ? *p.d_pos : p.pos) + t;
+    const bool active = blk < 2 * nblk && pos >= 0 && pos < p.max_ctx;
+    float x = active ? (float)xh : 0.0f;
+    if (__builtin_isnan(x)) x = 0.0f;
     float amax = fabsf(x);
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
