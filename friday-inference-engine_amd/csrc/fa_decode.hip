@@ -489,11 +489,11 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
             qf[s] = *reinterpret_cast<const h8*>(&raw);
         }
         if constexpr (!ROPE) return;
-        // Every load below is issued by every wave, whatever rot_q, the pair layout or the
-        // wave's role (loads it does not need go through a descriptor of size 0: zeros, no
-        // memory access). The compiler counts outstanding loads along each path; where paths
-        // with different load counts join it keeps the smallest count, and the waits of the
-        // q rotation then drained the first K/V tiles issued after these loads as well.
+        // The table entries of the q rotation are loaded by every wave whatever rot_q and the
+        // pair layout, and prepare() uses them unconditionally: the compiler counts
+        // outstanding loads along each path and keeps the smallest count where paths join,
+        // and it moves a load whose value is used in one branch only into that branch, behind
+        // the first K/V tiles; either made the rotation's waits drain those tiles too.
         const int pos = S > 0 ? S - 1 : 0;
         const float2* cs = reinterpret_cast<const float2*>(p.rope_table) + (size_t)pos * HD2;
         if constexpr (QREG) crow = cs[lane < HD2 ? lane : HD2 - 1];
