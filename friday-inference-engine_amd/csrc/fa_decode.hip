@@ -892,11 +892,12 @@ __global__ __launch_bounds__((WOV ? WOV : waves_for(PAGED, Q8, KPW)) * 64, WOV ?
             base = (unsigned)__builtin_amdgcn_raw_buffer_load_b32(rb, 0, 0, kCpolSc1);
         }
         using Whole = std::integral_constant<int, 0>;
-        if constexpr (ROPE && !Q8 && N > 1) {
-            // Short splits (all of a wave's tiles in flight at once): the first tile goes into
-            // LDS, and its stage's refill is issued, before the q rotation (whose loads and
-            // barrier it would otherwise wait behind); its QK then waits for the rotated q.
-            // (With one tile in flight per wave, measured 0.2 us slower at 32k: not used.)
+        if constexpr (ROPE && !Q8 && N > 1 && !QREG) {
+            // Paged short splits (all of a wave's tiles in flight at once): the first tile goes
+            // into LDS, and its stage's refill is issued, before the q rotation (whose barrier
+            // it would otherwise wait behind); its QK then waits for the rotated q. (With one
+            // tile in flight per wave, measured 0.2 us slower at 32k: not used.) Contiguous
+            // caches rotate in registers first, while the first tiles are in flight.
             if (groups > 0) consume(st[0], wt, wt + N * WT, std::integral_constant<int, 1>{});
             prepare();
             stamp(2);
