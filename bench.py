@@ -693,6 +693,45 @@ def paged_config(cx, steps, warmup, L=8):
             "tokens_per_s": round(B / (ms * 1e-3), 0)}
 
 
+def probe_configs(cx, steps, warmup, L=64):
+    """Read-pattern probes (bench_kit): the K/V access patterns of the decode kernels without
+    their arithmetic, 256 workgroups per launch, one launch per layer over 64 layers of
+    32768-row caches (cold: 8 GiB), timed like the headline (graph replays). They bound what a
+    decode launch of that pattern can stream; the empty kernel gives the launch floor."""
+    bk, fa = cx.bk, cx.fa
+    bk.fabk_probe_count.restype = C.c_int
+    bk.fabk_probe_name.restype = C.c_char_p
+    bk.fabk_probe_name.argtypes = [C.c_int]
+    bk.fabk_probe_row_bytes.argtypes = [C.c_int]
+    bk.fabk_probe_launch.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    S = 32768
+    lb = S * 2048
+    K, V, out = fa.DeviceBuffer(L * lb), fa.DeviceBuffer(L * lb), fa.DeviceBuffer(4096)
+    recs = []
+    try:
+        for v in range(-1, bk.fabk_probe_count()):
+            rowb = bk.fabk_probe_row_bytes(v)
+            layer = S * rowb
+
+            def run(v=v, layer=layer):
+                for l in range(L):
+                    if bk.fabk_probe_launch(v, C.c_void_p(K.ptr + l * layer), C.c_void_p(V.ptr + l * layer),
+                                            C.c_void_p(out.ptr), cx.stream.s) != 0:
+                        raise RuntimeError("probe launch failed")
+
+            us = cx.timed(run, steps, warmup) * 1e3 / L
+            rec = {"config": "probe: " + bk.fabk_probe_name(v).decode(), "us_per_launch": round(us, 3)}
+            if rowb:
+                gbs = 2 * layer / (us * 1e-6) / 1e9
+                rec.update({"bytes_per_launch": 2 * layer, "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+            recs.append(rec)
+            log(f"[bench] {rec}")
+    finally:
+        for b in (K, V, out):
+            b.free()
+    return recs
+
+
 STAMP_NAMES = ("entry", "ctx_known", "q_ready", "stream_end", "combine_done", "partials_stored", "counted",
                "merged")
 
@@ -774,7 +813,7 @@ def main():
                     help="only copy 1 GiB three times with the bench-kit streaming copy (one 16-byte load and "
                          "store per element): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run give the "
                          "counters' reading for a known 1 GiB read + 1 GiB write")
-    ap.add_argument("--config", choices=("headline", "all", "others", "short", "prefill", "paged", "q8", "gemm", "layer", "append", "stamps"), default="headline",
+    ap.add_argument("--config", choices=("headline", "all", "others", "short", "prefill", "paged", "q8", "gemm", "layer", "append", "stamps", "probe"), default="headline",
                     help="headline: the driver's one line; all/others: also (only) the other benchmark configs; "
                          "short: configs 1 and 2 only")
     args = ap.parse_args()
@@ -848,6 +887,9 @@ def main():
     if args.config == "layer":
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup)), flush=True)
         print(json.dumps(layer_block_config(cx, 32768, 64, args.steps, args.warmup, fused=True)), flush=True)
+    if args.config == "probe":
+        for rec in probe_configs(cx, args.steps, args.warmup):
+            print(json.dumps(rec), flush=True)
     if args.config == "stamps":
         for rec in (stamps_config(cx, "3: 40q/8kv x 64 layers", 32768, 64, 40, 8, 128, args.steps, args.warmup),
                     stamps_config(cx, "2: 32q/8kv x 32 layers", 1024, 32, 32, 8, 128, args.steps, args.warmup),
